@@ -1,0 +1,162 @@
+/*
+ * iq4xs_mi355x.h -- C ABI of the MI355X (gfx950) IQ4_XS x Q8_1 mul_mat library
+ * (libiq4xs_mi355x.so).
+ *
+ * Every entry point takes plain device pointers and sizes; `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream).  Return values are
+ * hipError_t codes as int:
+ *   IQ4XS_SUCCESS                 0  hipSuccess
+ *   IQ4XS_ERROR_INVALID_VALUE     1  hipErrorInvalidValue  (null pointer, K <= 0,
+ *                                    K % 256 != 0, N <= 0, M <= 0, bad layout,
+ *                                    workspace too small)
+ *   IQ4XS_ERROR_INVALID_CONFIG    9  hipErrorInvalidConfiguration (grid too large)
+ *   IQ4XS_ERROR_NOT_SUPPORTED   801  hipErrorNotSupported (e.g. shape not served)
+ * or any other hipError_t reported by the runtime.  Arguments are validated
+ * before anything is launched; a failing call launches nothing.
+ *
+ * Reference citations are file:line in the reference repository; "patch"
+ * means patches/0001-gfx1100-mul-mat-custom.patch.
+ *
+ * Data formats (byte-compatible with ggml):
+ *   W     : IQ4_XS, row-major [N][K/256] blocks of 136 bytes
+ *           (kernels/common/block_iq4_xs.h:10-19)
+ *   Q8_1  : 36-byte blocks {uint32 ds = fp16 d | fp16 sum << 16, int8 qs[32]}
+ *           (real_stock_dp4a_comparator.hip:22-26); d and sum are encoded with
+ *           round-toward-zero as the reference's pack_half2 (:43-62)
+ */
+#ifndef IQ4XS_MI355X_H
+#define IQ4XS_MI355X_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IQ4XS_SUCCESS 0
+#define IQ4XS_ERROR_INVALID_VALUE 1
+#define IQ4XS_ERROR_INVALID_CONFIG 9
+#define IQ4XS_ERROR_NOT_SUPPORTED 801
+
+#define IQ4XS_QK_K 256
+#define IQ4XS_QK8_1 32
+#define IQ4XS_BLOCK_BYTES 136
+#define IQ4XS_Q8_1_BLOCK_BYTES 36
+#define IQ4XS_GGML_TYPE_IQ4_XS 23 /* ggml_type value of GGML_TYPE_IQ4_XS */
+
+/* Activation / output layouts */
+#define IQ4XS_LAYOUT_KM 0 /* X[k*M + m], Y[n*M + m]  (standalone kernels/matmul_iq4xs API) */
+#define IQ4XS_LAYOUT_MK 1 /* X[m*K + k], Y[m*N + n]  (ggml src1 / dst)                    */
+
+/* Kernel selection for iq4xs_mul_mat_q8_1 / iq4xs_subblock_sums */
+#define IQ4XS_PATH_AUTO -1 /* streaming GEMV for M <= 8, int8-MFMA GEMM above */
+#define IQ4XS_PATH_GEMV 0  /* streaming GEMV (M <= 8 only)                   */
+#define IQ4XS_PATH_GEMM 1  /* int8-MFMA GEMM (any M)                         */
+
+/* ===================== standalone API (kernels/matmul_iq4xs) ===================== */
+
+/* Replaces quantize_row_q8_1_gpu, real_stock_dp4a_comparator.hip:266-273.
+ * x[K] fp32 -> y[K/32] Q8_1 blocks.  K % 32 == 0. */
+int quantize_row_q8_1_gpu(const float* x, void* y, int64_t K, void* stream);
+
+/* Replaces quantize_row_q8_1_batched_gpu, real_stock_dp4a_comparator.hip:308-315.
+ * X[k*M + m] -> Y[m*(K/32) + ib].  K % 32 == 0. */
+int quantize_row_q8_1_batched_gpu(const float* X, void* Y, int64_t K, int64_t M, void* stream);
+
+/* Replaces gemv_iq4xs_stock_dp4a_gpu, real_stock_dp4a_comparator.hip:480-503:
+ * y[N] = W x (x quantised to Q8_1 first).  The Q8_1 scratch comes from the
+ * device's stream-ordered pool (hipMallocAsync/hipFreeAsync on `stream`): no
+ * device-wide synchronisation, unlike the reference's hipMalloc/hipFree. */
+int gemv_iq4xs_stock_dp4a_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
+
+/* Replaces the C-linkage gemv_iq4xs_dp4a_coop_gpu, impl_gemv_dp4a_gfx1100.hip:332-341
+ * (same contract as gemv_iq4xs_stock_dp4a_gpu). */
+int gemv_iq4xs_dp4a_coop_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
+
+/* Replaces gemm_iq4xs_stock_dp4a_gpu, real_stock_dp4a_comparator.hip:505-548:
+ * Y[n*M + m] = sum_k W[n,k] X[k*M + m].  M <= 8 runs the streaming GEMV,
+ * larger M the int8-MFMA GEMM. */
+int gemm_iq4xs_stock_dp4a_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                              void* stream);
+
+/* ============================ ggml mul_mat boundary ============================ */
+
+/* Replaces custom_gemv_iq4xs_can_handle, patch:274-277.  True for
+ * type == GGML_TYPE_IQ4_XS, 1 <= M <= 8, K > 0, K % 256 == 0, N > 0 (the
+ * reference's K/N whitelist is dropped). */
+bool custom_gemv_iq4xs_can_handle(int64_t K, int64_t N, int64_t M, int type);
+
+/* Replaces custom_gemv_iq4xs_dispatch, patch:278-280 (called from the mmvq.cu
+ * hook, patch:327-334): y[N] = W x for ggml's src0/src1/dst of one column.
+ * Stream-ordered; no host synchronisation (the reference synchronises the
+ * stream and refuses graph capture, patch:269-272). */
+int custom_gemv_iq4xs_dispatch(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
+
+/* Replaces custom_gemm_iq4xs_can_handle, patch:148-151: type == IQ4_XS,
+ * M >= 1, K > 0, K % 256 == 0, N > 0. */
+bool custom_gemm_iq4xs_can_handle(int64_t K, int64_t N, int64_t M, int type);
+
+/* Replaces custom_gemm_iq4xs_dispatch, patch:152-154 (mmq.cu hook,
+ * patch:299-306): ggml layout X[m*K + k] -> Y[m*N + n]. */
+int custom_gemm_iq4xs_dispatch(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                               void* stream);
+
+/* ====================== explicit-workspace API (capture-safe) ======================
+ * No counterpart in the reference (which allocates per call, e.g.
+ * real_stock_dp4a_comparator.hip:491,501).  For callers that own their memory:
+ * the calls below allocate nothing and never synchronise.  The workspace holds
+ * Q8_1 activations in planar form: int8 codes [M][K] at offset 0, then the
+ * uint32 ds words [M][K/32] at a 256-byte aligned offset. */
+
+/* Bytes of workspace for M activation columns of length K. */
+size_t iq4xs_workspace_bytes(int64_t K, int64_t M);
+
+/* X (layout IQ4XS_LAYOUT_KM or _MK) -> planar Q8_1 in ws. */
+int iq4xs_quantize_q8_1(const float* X, int64_t K, int64_t M, int layout, void* ws, size_t ws_bytes,
+                        void* stream);
+
+/* Y = W * dequant(ws) from an already quantised workspace; `layout` selects
+ * the Y layout; `path` is one of IQ4XS_PATH_*. */
+int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                       int path, void* stream);
+
+/* Quantise + multiply in one call. */
+int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
+                  size_t ws_bytes, void* stream);
+
+/* ================================ debug exports ================================
+ * No counterpart in the reference; they exist so the Q8_1 blocks and the
+ * per-32-element int32 sums can be checked bit for bit. */
+
+/* Planar workspace -> M*(K/32) 36-byte Q8_1 blocks (block (m, ib) at m*(K/32)+ib). */
+int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, void* stream);
+
+/* S[(m*N + n)*(K/32) + kb] = sumi * (ls - 32) of sub-block kb, row n, column m,
+ * computed by the production kernel selected by `path` (IQ4XS_PATH_GEMV or
+ * _GEMM: the same device code as iq4xs_mul_mat_q8_1, with one extra store).
+ * The kernel also writes its outputs to Y (M*N floats, layout IQ4XS_LAYOUT_MK). */
+int iq4xs_subblock_sums(const void* W, const void* ws, int32_t* S, float* Y, int64_t K, int64_t N, int64_t M,
+                        int path, void* stream);
+
+/* One v_mfma_i32_32x32x32_i8 through the GEMM's operand layouts:
+ * C[i*32 + j] = sum_k A[i*32 + k] * B[j*32 + k]. */
+int iq4xs_probe_mfma_i8(const int8_t* A, const int8_t* B, int32_t* C, void* stream);
+
+/* ============================ synthetic inputs ============================ */
+
+/* n_blocks IQ4_XS blocks made on the device from `seed` (block i is the
+ * recipe's block first_block + i). */
+int iq4xs_fill_synthetic_weights(void* W, int64_t n_blocks, uint64_t seed, int64_t first_block, void* stream);
+
+/* n fp32 activations ~ N(0,1); outliers != 0 scales 1 % of them x20. */
+int iq4xs_fill_synthetic_activations(float* x, int64_t n, uint64_t seed, int outliers, void* stream);
+
+/* Library version string. */
+const char* iq4xs_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

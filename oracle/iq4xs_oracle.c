@@ -1,0 +1,376 @@
+/*
+ * iq4xs_oracle.c -- CPU restatement of the reference IQ4_XS x Q8_1 path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker).  See iq4xs_oracle.h for what pins
+ * each function.  Built with -ffp-contract=off so that every float expression
+ * rounds exactly as written, like the reference's scalar code.
+ */
+#include "iq4xs_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* kernels/common/block_iq4_xs.h:22-24 */
+const int8_t orc_kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                       1,    13,   25,  38,  53,  69,  89,  113};
+
+/* kernels/common/block_iq4_xs.h:34-68 -- exact IEEE binary16 -> binary32. */
+float orc_fp16_to_fp32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            /* subnormal: value = m * 2^-24; renormalise */
+            int shift = 0;
+            while ((m & 0x400u) == 0) {
+                m <<= 1;
+                ++shift;
+            }
+            m &= 0x3FFu;
+            bits = sign | ((uint32_t)(127 - 15 + 1 - shift) << 23) | (m << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 127 - 15) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+/*
+ * kernels/common/block_iq4_xs.h:71-86 and real_stock_dp4a_comparator.hip:43-62
+ * (pack_half2's f32_to_f16_bits): mantissa truncated (round toward zero),
+ * |x| < 2^-24 flushes to signed zero, biased exponent >= 31 (|x| >= 65536,
+ * Inf, NaN) saturates to signed Inf.
+ */
+uint16_t orc_fp32_to_fp16_trunc(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t e = (int32_t)((x >> 23) & 0xFFu) - 127 + 15;
+    uint32_t m = (x >> 13) & 0x3FFu;
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        return (uint16_t)(sign | ((m | 0x400u) >> (1 - e)));
+    }
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | ((uint32_t)e << 10) | m);
+}
+
+void orc_fp16_to_fp32_array(const uint16_t* h, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_fp16_to_fp32(h[i]);
+}
+
+void orc_fp32_to_fp16_trunc_array(const float* f, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_fp32_to_fp16_trunc(f[i]);
+}
+
+/* kernels/matmul_iq4xs/ref_cpu.cpp:28-31: 6-bit scale of sub-block ib, 0..63. */
+int orc_subblock_scale(const orc_block_iq4_xs* b, int ib) {
+    int lo = (b->scales_l[ib / 2] >> (4 * (ib & 1))) & 0x0F;
+    int hi = (b->scales_h >> (2 * ib)) & 0x03;
+    return lo | (hi << 4);
+}
+
+static uint32_t pack_half2_trunc(float lo, float hi) {
+    return (uint32_t)orc_fp32_to_fp16_trunc(lo) | ((uint32_t)orc_fp32_to_fp16_trunc(hi) << 16);
+}
+
+/*
+ * real_stock_dp4a_comparator.hip:230-264 -- DEVICE semantics of one Q8_1
+ * block (not the host helper at :204-227, which multiplies by 1/d and sums
+ * sequentially).  32 lanes hold x[0..31]; five xor-butterfly steps with
+ * offsets 16,8,4,2,1 reduce amax and sum; every lane then holds the same
+ * values.  d = amax/127 (true division), q = roundf(x/d), ds = trunc-half2.
+ */
+static void quantize_block(const float* xs, ptrdiff_t stride, orc_block_q8_1* out) {
+    float amax[32], sum[32], x[32];
+    for (int t = 0; t < 32; ++t) {
+        x[t] = xs[t * stride];
+        amax[t] = fabsf(x[t]);
+        sum[t] = x[t];
+    }
+    for (int off = 16; off > 0; off >>= 1) {
+        float na[32], ns[32];
+        for (int t = 0; t < 32; ++t) {
+            na[t] = fmaxf(amax[t], amax[t ^ off]);
+            ns[t] = sum[t] + sum[t ^ off];
+        }
+        memcpy(amax, na, sizeof na);
+        memcpy(sum, ns, sizeof ns);
+    }
+    const float a = amax[0];
+    const float d = a / 127.0f;
+    for (int t = 0; t < 32; ++t) {
+        out->qs[t] = (a != 0.0f) ? (int8_t)roundf(x[t] / d) : (int8_t)0;
+    }
+    out->ds = pack_half2_trunc(d, sum[0]);
+}
+
+/* real_stock_dp4a_comparator.hip:230-273 (one row x[K] -> K/32 blocks). */
+void orc_quantize_q8_1(const float* x, orc_block_q8_1* y, int64_t K) {
+    const int64_t nb = K / ORC_QK8_1;
+    for (int64_t ib = 0; ib < nb; ++ib) quantize_block(x + ib * ORC_QK8_1, 1, y + ib);
+}
+
+/*
+ * real_stock_dp4a_comparator.hip:278-306 -- batched: column m of X quantised
+ * into Y[m*nb + ib].  layout ORC_LAYOUT_KM reads X[k*M+m] (standalone API),
+ * ORC_LAYOUT_MK reads X[m*K+k] (ggml src1).
+ */
+void orc_quantize_q8_1_batched(const float* X, orc_block_q8_1* Y, int64_t K, int64_t M, int layout) {
+    const int64_t nb = K / ORC_QK8_1;
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t ib = 0; ib < nb; ++ib) {
+            const int64_t k0 = ib * ORC_QK8_1;
+            if (layout == ORC_LAYOUT_KM)
+                quantize_block(X + k0 * M + m, (ptrdiff_t)M, Y + m * nb + ib);
+            else
+                quantize_block(X + m * K + k0, 1, Y + m * nb + ib);
+        }
+    }
+}
+
+/* x_hat = fp16(d) * q : the values a Q8_1 path actually multiplies. */
+void orc_dequant_q8_1(const orc_block_q8_1* y, float* xhat, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; ++b) {
+        const float d = orc_fp16_to_fp32((uint16_t)(y[b].ds & 0xFFFFu));
+        for (int t = 0; t < 32; ++t) xhat[b * 32 + t] = d * (float)y[b].qs[t];
+    }
+}
+
+static inline int32_t dot4_i8(uint32_t a, uint32_t b, int32_t c) {
+    for (int i = 0; i < 4; ++i) c += (int32_t)(int8_t)(a >> (8 * i)) * (int32_t)(int8_t)(b >> (8 * i));
+    return c;
+}
+
+static inline uint32_t load_u32(const void* p) {
+    uint32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+
+/*
+ * real_stock_dp4a_comparator.hip:145-166 with :105-131 and :68-88 -- integer
+ * part of vec_dot_iq4_xs_q8_1 for sub-block ib (iqs = 4*ib): qs word iqs+j
+ * gives 4 low-nibble codes (weights 4j..4j+3, paired with q8 word j) and 4
+ * high-nibble codes (weights 16+4j.., paired with q8 word j+4); the sum is
+ * then multiplied by (ls - 32).  bq8_chunk points at the 8 Q8_1 blocks of the
+ * super-block.
+ */
+int32_t orc_subblock_sumi(const orc_block_iq4_xs* bq4, const orc_block_q8_1* bq8_chunk, int ib) {
+    const orc_block_q8_1* a = bq8_chunk + ib;
+    int32_t sumi = 0;
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t q4 = load_u32(bq4->qs + 16 * ib + 4 * j);
+        uint32_t vx = 0, vy = 0;
+        for (int i = 0; i < 4; ++i) {
+            vx |= (uint32_t)(uint8_t)orc_kvalues_iq4nl[(q4 >> (8 * i)) & 0xF] << (8 * i);
+            vy |= (uint32_t)(uint8_t)orc_kvalues_iq4nl[(q4 >> (8 * i + 4)) & 0xF] << (8 * i);
+        }
+        sumi = dot4_i8(vx, load_u32(a->qs + 4 * j), sumi);
+        sumi = dot4_i8(vy, load_u32(a->qs + 4 * j + 16), sumi);
+    }
+    return sumi * (orc_subblock_scale(bq4, ib) - 32);
+}
+
+/* S[(m*N + n)*(K/32) + kb]: scaled int32 sum of every 32-element sub-block. */
+void orc_subblock_sums(const orc_block_iq4_xs* W, const orc_block_q8_1* AQ, int32_t* S,
+                       int64_t K, int64_t N, int64_t M) {
+    const int64_t bpr = K / ORC_QK_K, nb = K / ORC_QK8_1;
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t b = 0; b < bpr; ++b)
+                for (int ib = 0; ib < 8; ++ib)
+                    S[(m * N + n) * nb + b * 8 + ib] =
+                        orc_subblock_sumi(W + n * bpr + b, AQ + m * nb + b * 8, ib);
+}
+
+/* real_stock_dp4a_comparator.hip:160-165: fp32 term of one sub-block. */
+static inline float subblock_term(const orc_block_iq4_xs* bq4, const orc_block_q8_1* chunk, int ib) {
+    const int32_t sumi = orc_subblock_sumi(bq4, chunk, ib);
+    const float d = orc_fp16_to_fp32(bq4->d) * orc_fp16_to_fp32((uint16_t)(chunk[ib].ds & 0xFFFFu));
+    return d * (float)sumi;
+}
+
+/*
+ * real_stock_dp4a_comparator.hip:325-360 -- fp32 output of the reference
+ * GEMV kernel, in its order: lane t (0..31) sums super-blocks t/8, t/8+4, ...
+ * at sub-block t%8, then a 16,8,4,2,1 xor butterfly; lane 0 stores.
+ */
+void orc_gemv_semantics(const orc_block_iq4_xs* W, const orc_block_q8_1* AQ, float* y,
+                        int64_t K, int64_t N) {
+    const int64_t bpr = K / ORC_QK_K;
+    for (int64_t r = 0; r < N; ++r) {
+        float tmp[32];
+        for (int t = 0; t < 32; ++t) {
+            float acc = 0.0f;
+            for (int64_t kbx = t / 8; kbx < bpr; kbx += 4)
+                acc += subblock_term(W + r * bpr + kbx, AQ + kbx * 8, t % 8);
+            tmp[t] = acc;
+        }
+        for (int off = 16; off > 0; off >>= 1) {
+            float nt[32];
+            for (int t = 0; t < 32; ++t) nt[t] = tmp[t] + tmp[t ^ off];
+            memcpy(tmp, nt, sizeof nt);
+        }
+        y[r] = tmp[0];
+    }
+}
+
+/*
+ * real_stock_dp4a_comparator.hip:374-443 (tiled GEMM, same per-element order
+ * as the simple kernel :446-472): acc over super-blocks, then sub-blocks.
+ * AQ is [M][K/32] blocks; Y[n*M + m].
+ */
+void orc_gemm_semantics(const orc_block_iq4_xs* W, const orc_block_q8_1* AQ, float* Y,
+                        int64_t K, int64_t N, int64_t M) {
+    const int64_t bpr = K / ORC_QK_K, nb = K / ORC_QK8_1;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t m = 0; m < M; ++m) {
+            float acc = 0.0f;
+            for (int64_t kbx = 0; kbx < bpr; ++kbx)
+                for (int ib = 0; ib < 8; ++ib)
+                    acc += subblock_term(W + n * bpr + kbx, AQ + m * nb + kbx * 8, ib);
+            Y[n * M + m] = acc;
+        }
+}
+
+/*
+ * kernels/matmul_iq4xs/ref_cpu.cpp:12-52 -- FP64 oracle GEMV:
+ * dl = double(d) * double(float(ls) - 32), w = dl * kvalue, acc += w * x.
+ */
+static double row_dot_fp64(const orc_block_iq4_xs* row, const float* x, ptrdiff_t xstride, int64_t bpr) {
+    double acc = 0.0;
+    for (int64_t b = 0; b < bpr; ++b) {
+        const float d = orc_fp16_to_fp32(row[b].d);
+        for (int ib = 0; ib < 8; ++ib) {
+            const double dl = (double)d * (double)((float)orc_subblock_scale(row + b, ib) - 32.0f);
+            const uint8_t* qs = row[b].qs + ib * 16;
+            const int64_t k0 = b * ORC_QK_K + ib * 32;
+            for (int j = 0; j < 16; ++j) {
+                const double wlo = dl * (double)orc_kvalues_iq4nl[qs[j] & 0x0F];
+                const double whi = dl * (double)orc_kvalues_iq4nl[(qs[j] >> 4) & 0x0F];
+                acc += wlo * (double)x[(k0 + j) * xstride];
+                acc += whi * (double)x[(k0 + j + 16) * xstride];
+            }
+        }
+    }
+    return acc;
+}
+
+void orc_gemv_fp64(const orc_block_iq4_xs* W, const float* x, float* y, int64_t K, int64_t N) {
+    const int64_t bpr = K / ORC_QK_K;
+    for (int64_t r = 0; r < N; ++r) y[r] = (float)row_dot_fp64(W + r * bpr, x, 1, bpr);
+}
+
+/*
+ * kernels/matmul_iq4xs/ref_cpu.cpp:54-106 -- FP64 oracle GEMM, X[k*M+m],
+ * Y[n*M+m]; same per-element order as the GEMV.  Rows are split over
+ * nthreads OpenMP threads; each element's arithmetic is unchanged, so the
+ * result is identical for every thread count.
+ */
+void orc_gemm_fp64(const orc_block_iq4_xs* W, const float* X, float* Y, int64_t K, int64_t N,
+                   int64_t M, int nthreads) {
+    const int64_t bpr = K / ORC_QK_K;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads > 0 ? nthreads : 1)
+#endif
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t m = 0; m < M; ++m)
+            Y[n * M + m] = (float)row_dot_fp64(W + n * bpr, X + m, (ptrdiff_t)M, bpr);
+}
+
+/* kernels/matmul_iq4xs/ref_cpu.cpp:108-139 -- fp32 dequantisation. */
+void orc_dequant(const orc_block_iq4_xs* W, float* out, int64_t K, int64_t N) {
+    const int64_t bpr = K / ORC_QK_K;
+    for (int64_t r = 0; r < N; ++r)
+        for (int64_t b = 0; b < bpr; ++b) {
+            const orc_block_iq4_xs* blk = W + r * bpr + b;
+            const float d = orc_fp16_to_fp32(blk->d);
+            for (int ib = 0; ib < 8; ++ib) {
+                const float dl = d * ((float)orc_subblock_scale(blk, ib) - 32.0f);
+                float* o = out + r * K + b * ORC_QK_K + ib * 32;
+                for (int j = 0; j < 16; ++j) {
+                    o[j] = dl * (float)orc_kvalues_iq4nl[blk->qs[ib * 16 + j] & 0x0F];
+                    o[j + 16] = dl * (float)orc_kvalues_iq4nl[(blk->qs[ib * 16 + j] >> 4) & 0x0F];
+                }
+            }
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Seeded synthetic inputs.  Counter-based, so any block/element can be made
+ * independently (the product library's device generator makes the same
+ * weights bit for bit).  splitmix64 finaliser: Steele, Lea, Flood, "Fast
+ * splittable pseudorandom number generators", OOPSLA 2014.                   */
+
+static inline uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static inline uint64_t draw(uint64_t seed, uint64_t stream, uint64_t ctr) {
+    return mix64(mix64(seed ^ (stream * 0xD1B54A32D192ED03ull)) ^ ctr);
+}
+
+/*
+ * Weights per the synthetic recipe: fp16 d ~ U(0.005, 0.02) (stored with the
+ * reference's truncating encoder, kernels/common/matmul_test_util.h:58),
+ * eight 6-bit sub-block scales uniform in 0..63, codebook indices uniform
+ * over the 16 entries.  Block g (global index first_block + i) uses draws
+ * 18g .. 18g+17 of stream 1.
+ */
+void orc_gen_weights(orc_block_iq4_xs* W, int64_t n_blocks, uint64_t seed, int64_t first_block) {
+    for (int64_t i = 0; i < n_blocks; ++i) {
+        const uint64_t g = (uint64_t)(first_block + i);
+        orc_block_iq4_xs* b = W + i;
+        const uint64_t r0 = draw(seed, 1, g * 18 + 0);
+        const float t = (float)(uint32_t)(r0 >> 40) * 8.94069671630859375e-10f; /* 0.015 / 2^24 */
+        b->d = orc_fp32_to_fp16_trunc(t + 0.005f);
+        const uint64_t r1 = draw(seed, 1, g * 18 + 1);
+        uint16_t sh = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+            const unsigned ls = (unsigned)(r1 >> (6 * ib)) & 63u;
+            if ((ib & 1) == 0)
+                b->scales_l[ib / 2] = (uint8_t)(ls & 0xF);
+            else
+                b->scales_l[ib / 2] |= (uint8_t)((ls & 0xF) << 4);
+            sh |= (uint16_t)((ls >> 4) << (2 * ib));
+        }
+        b->scales_h = sh;
+        for (int w = 0; w < 16; ++w) {
+            const uint64_t r = draw(seed, 1, g * 18 + 2 + (uint64_t)w);
+            memcpy(b->qs + 8 * w, &r, 8);
+        }
+    }
+}
+
+/*
+ * Activations: x_i ~ N(0,1) by Box-Muller on draws i of streams 2 and 3;
+ * with outliers != 0, element i is scaled x20 when draw i of stream 4 is
+ * 0 mod 100 (1 % of positions, seeded).
+ */
+void orc_gen_activations(float* x, int64_t n, uint64_t seed, int outliers) {
+    const double two_pi = 6.283185307179586476925286766559;
+    for (int64_t i = 0; i < n; ++i) {
+        const double u1 = (double)((draw(seed, 2, (uint64_t)i) >> 11) + 1) * 0x1.0p-53;
+        const double u2 = (double)(draw(seed, 3, (uint64_t)i) >> 11) * 0x1.0p-53;
+        float v = (float)(sqrt(-2.0 * log(u1)) * cos(two_pi * u2));
+        if (outliers && draw(seed, 4, (uint64_t)i) % 100 == 0) v *= 20.0f;
+        x[i] = v;
+    }
+}

@@ -1,0 +1,193 @@
+// c_api.hip -- the extern "C" boundary declared in include/iq4xs_mi355x.h.
+// Argument checks mirror the reference launchers (hipErrorInvalidValue for
+// null pointers and bad shapes, real_stock_dp4a_comparator.hip:487,513;
+// impl_gemv_dp4a_gfx1100.hip:299-300) and run before anything is launched.
+#include <mutex>
+#include <vector>
+
+#include "iq4xs_device.h"
+#include "iq4xs_internal.h"
+#include "iq4xs_mi355x.h"
+
+using namespace iq4xs;
+
+namespace {
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool valid_k(int64_t K) { return K > 0 && K % QK_K == 0; }
+
+// Largest tensor the int32/int64 index arithmetic of the kernels is sized for.
+constexpr int64_t MAX_DIM = (int64_t)1 << 31;
+
+bool valid_mat(const void* W, const void* X, const void* Y, int64_t K, int64_t N, int64_t M) {
+    return W && X && Y && valid_k(K) && N > 0 && M > 0 && K < MAX_DIM && N < MAX_DIM && M < MAX_DIM;
+}
+
+// The stream-ordered pool of each device keeps freed blocks instead of
+// returning them to the driver, so per-call scratch is a pool hit.
+std::once_flag g_pool_once[64];
+
+hipError_t pool_alloc(void** p, size_t bytes, hipStream_t stream) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev >= 0 && dev < 64) {
+        std::call_once(g_pool_once[dev], [dev]() {
+            hipMemPool_t pool;
+            if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+                uint64_t keep = UINT64_MAX;
+                (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+            }
+        });
+    }
+    return hipMallocAsync(p, bytes, stream);
+}
+
+struct Planar {
+    int8_t* qs;
+    uint32_t* ds;
+};
+
+Planar planar_view(const void* ws, int64_t K, int64_t M) {
+    uint8_t* base = static_cast<uint8_t*>(const_cast<void*>(ws));
+    return {reinterpret_cast<int8_t*>(base), reinterpret_cast<uint32_t*>(base + planar_ds_offset(K, M))};
+}
+
+hipError_t mul_mat_planar(const uint8_t* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                          int path, int32_t* dbg, hipStream_t stream) {
+    const Planar p = planar_view(ws, K, M);
+    const int64_t ldy_m = (layout == LAYOUT_MK) ? N : 1;
+    const int64_t ldy_n = (layout == LAYOUT_MK) ? 1 : M;
+    if (path == IQ4XS_PATH_AUTO) path = (M <= GEMV_MAX_COLS) ? IQ4XS_PATH_GEMV : IQ4XS_PATH_GEMM;
+    if (path == IQ4XS_PATH_GEMV) {
+        if (M > GEMV_MAX_COLS) return hipErrorInvalidValue;
+        return launch_gemv(W, p.qs, p.ds, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
+    }
+    if (path == IQ4XS_PATH_GEMM) return launch_gemm(W, p.qs, p.ds, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
+    return hipErrorInvalidValue;
+}
+
+// quantise + multiply with scratch from the stream-ordered pool
+hipError_t mul_mat_pooled(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                          hipStream_t stream) {
+    if (!valid_mat(W, X, Y, K, N, M)) return hipErrorInvalidValue;
+    void* ws = nullptr;
+    hipError_t err = pool_alloc(&ws, planar_bytes(K, M), stream);
+    if (err != hipSuccess) return err;
+    const Planar p = planar_view(ws, K, M);
+    err = launch_quantize(X, K, M, layout, p.qs, p.ds, nullptr, stream);
+    if (err == hipSuccess)
+        err = mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, IQ4XS_PATH_AUTO, nullptr,
+                             stream);
+    const hipError_t ferr = hipFreeAsync(ws, stream);
+    return err != hipSuccess ? err : ferr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int quantize_row_q8_1_gpu(const float* x, void* y, int64_t K, void* stream) {
+    if (!x || !y || K <= 0 || K % QK8_1 != 0 || K >= MAX_DIM) return hipErrorInvalidValue;
+    return launch_quantize(x, K, 1, LAYOUT_MK, nullptr, nullptr, static_cast<block_q8_1*>(y), as_stream(stream));
+}
+
+int quantize_row_q8_1_batched_gpu(const float* X, void* Y, int64_t K, int64_t M, void* stream) {
+    if (!X || !Y || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
+    return launch_quantize(X, K, M, LAYOUT_KM, nullptr, nullptr, static_cast<block_q8_1*>(Y), as_stream(stream));
+}
+
+int gemv_iq4xs_stock_dp4a_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream) {
+    return mul_mat_pooled(W, x, y, K, N, 1, LAYOUT_MK, as_stream(stream));
+}
+
+int gemv_iq4xs_dp4a_coop_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream) {
+    return mul_mat_pooled(W, x, y, K, N, 1, LAYOUT_MK, as_stream(stream));
+}
+
+int gemm_iq4xs_stock_dp4a_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                              void* stream) {
+    return mul_mat_pooled(W, X, Y, K, N, M, LAYOUT_KM, as_stream(stream));
+}
+
+bool custom_gemv_iq4xs_can_handle(int64_t K, int64_t N, int64_t M, int type) {
+    return type == IQ4XS_GGML_TYPE_IQ4_XS && M >= 1 && M <= GEMV_MAX_COLS && valid_k(K) && K < MAX_DIM && N > 0 &&
+           N < MAX_DIM;
+}
+
+int custom_gemv_iq4xs_dispatch(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream) {
+    return mul_mat_pooled(W, x, y, K, N, 1, LAYOUT_MK, as_stream(stream));
+}
+
+bool custom_gemm_iq4xs_can_handle(int64_t K, int64_t N, int64_t M, int type) {
+    return type == IQ4XS_GGML_TYPE_IQ4_XS && M >= 1 && M < MAX_DIM && valid_k(K) && K < MAX_DIM && N > 0 &&
+           N < MAX_DIM;
+}
+
+int custom_gemm_iq4xs_dispatch(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                               void* stream) {
+    return mul_mat_pooled(W, X, Y, K, N, M, LAYOUT_MK, as_stream(stream));
+}
+
+size_t iq4xs_workspace_bytes(int64_t K, int64_t M) {
+    if (K <= 0 || K % QK8_1 != 0 || M <= 0) return 0;
+    return planar_bytes(K, M);
+}
+
+int iq4xs_quantize_q8_1(const float* X, int64_t K, int64_t M, int layout, void* ws, size_t ws_bytes,
+                        void* stream) {
+    if (!X || !ws || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
+    if ((layout != LAYOUT_KM && layout != LAYOUT_MK) || ws_bytes < planar_bytes(K, M)) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
+    const Planar p = planar_view(ws, K, M);
+    return launch_quantize(X, K, M, layout, p.qs, p.ds, nullptr, as_stream(stream));
+}
+
+int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                       int path, void* stream) {
+    if (!valid_mat(W, ws, Y, K, N, M) || (layout != LAYOUT_KM && layout != LAYOUT_MK)) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
+    return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, path, nullptr, as_stream(stream));
+}
+
+int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
+                  size_t ws_bytes, void* stream) {
+    if (!valid_mat(W, X, Y, K, N, M) || !ws) return hipErrorInvalidValue;
+    const int err = iq4xs_quantize_q8_1(X, K, M, layout, ws, ws_bytes, stream);
+    if (err != hipSuccess) return err;
+    return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, IQ4XS_PATH_AUTO, nullptr,
+                          as_stream(stream));
+}
+
+int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, void* stream) {
+    if (!ws || !blocks || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
+    const Planar p = planar_view(ws, K, M);
+    return launch_planar_to_blocks(p.qs, p.ds, K, M, static_cast<block_q8_1*>(blocks), as_stream(stream));
+}
+
+int iq4xs_subblock_sums(const void* W, const void* ws, int32_t* S, float* Y, int64_t K, int64_t N, int64_t M,
+                        int path, void* stream) {
+    if (!valid_mat(W, ws, Y, K, N, M) || !S) return hipErrorInvalidValue;
+    if (path != IQ4XS_PATH_GEMV && path != IQ4XS_PATH_GEMM) return hipErrorInvalidValue;
+    return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, LAYOUT_MK, path, S, as_stream(stream));
+}
+
+int iq4xs_probe_mfma_i8(const int8_t* A, const int8_t* B, int32_t* C, void* stream) {
+    if (!A || !B || !C) return hipErrorInvalidValue;
+    return launch_probe_mfma(A, B, C, as_stream(stream));
+}
+
+int iq4xs_fill_synthetic_weights(void* W, int64_t n_blocks, uint64_t seed, int64_t first_block, void* stream) {
+    if (!W || n_blocks <= 0 || first_block < 0) return hipErrorInvalidValue;
+    return launch_fill_weights(static_cast<uint8_t*>(W), n_blocks, seed, first_block, as_stream(stream));
+}
+
+int iq4xs_fill_synthetic_activations(float* x, int64_t n, uint64_t seed, int outliers, void* stream) {
+    if (!x || n <= 0) return hipErrorInvalidValue;
+    return launch_fill_activations(x, n, seed, outliers, as_stream(stream));
+}
+
+const char* iq4xs_version(void) { return "iq4xs_mi355x 0.1.0 gfx950"; }
+
+}  // extern "C"

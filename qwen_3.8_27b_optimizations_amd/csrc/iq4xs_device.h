@@ -1,0 +1,138 @@
+// iq4xs_device.h -- IQ4_XS / Q8_1 formats and the register-level arithmetic
+// shared by every gfx950 kernel of this library.
+//
+// Formats (byte-compatible with ggml):
+//   block_iq4_xs  kernels/common/block_iq4_xs.h:10-19   136 B / 256 weights
+//   block_q8_1    real_stock_dp4a_comparator.hip:22-26   36 B / 32 activations
+//
+// Inside the library, quantised activations live in a "planar" Q8_1 buffer:
+//   qs : int8   [M][K]      (256-byte aligned)
+//   ds : uint32 [M][K/32]   ({trunc-fp16 d, trunc-fp16 sum}, ggml's ds word)
+// so that a lane reads its 32 codes with two aligned 16-byte loads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace iq4xs {
+
+constexpr int QK_K = 256;
+constexpr int QK8_1 = 32;
+constexpr int BLOCK_BYTES = 136;
+constexpr int Q8_1_BYTES = 36;
+
+struct __attribute__((packed)) block_iq4_xs {
+    uint16_t d;
+    uint16_t scales_h;
+    uint8_t scales_l[4];
+    uint8_t qs[128];
+};
+static_assert(sizeof(block_iq4_xs) == BLOCK_BYTES, "block_iq4_xs is 136 bytes");
+
+struct block_q8_1 {
+    uint32_t ds;
+    int8_t qs[QK8_1];
+};
+static_assert(sizeof(block_q8_1) == Q8_1_BYTES, "block_q8_1 is 36 bytes");
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+// 16-byte vector whose address is only known to be 8-byte aligned (the qs of
+// every other 136-byte super-block); gfx950 loads it with one dwordx4.
+typedef int v4i_a8 __attribute__((ext_vector_type(4), aligned(8)));
+
+// Byte offset of the planar ds array inside a Q8_1 workspace of M columns.
+__host__ __device__ inline size_t planar_ds_offset(int64_t K, int64_t M) {
+    return ((size_t)(K * M) + 255u) & ~(size_t)255u;
+}
+__host__ __device__ inline size_t planar_bytes(int64_t K, int64_t M) {
+    return planar_ds_offset(K, M) + (size_t)M * (size_t)(K / QK8_1) * 4u;
+}
+
+// Exact binary16 -> binary32 (hardware conversion; fp16 denormals are kept).
+__device__ inline float half_bits_to_float(uint32_t h) {
+    union {
+        uint16_t u;
+        _Float16 f;
+    } v;
+    v.u = (uint16_t)h;
+    return (float)v.f;
+}
+
+// binary32 -> binary16 rounding toward zero, |x| < 2^-24 -> signed zero,
+// |x| >= 65536 / Inf / NaN -> signed Inf.  This is the encoder the reference
+// uses for Q8_1 ds (real_stock_dp4a_comparator.hip:43-62); written here as
+// integer field arithmetic.
+__host__ __device__ inline uint32_t float_to_half_bits_rtz(float f) {
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int e = (int)((x >> 23) & 0xFFu) - 112;  // rebias 127 -> 15
+    const uint32_t m10 = (x >> 13) & 0x3FFu;
+    if (e >= 31) return sign | 0x7C00u;
+    if (e > 0) return sign | ((uint32_t)e << 10) | m10;
+    if (e < -10) return sign;
+    return sign | ((m10 | 0x400u) >> (1 - e));
+}
+
+// 6-bit scale of sub-block ib from the first 8 bytes of a super-block
+// (h0 = d | scales_h << 16, h1 = scales_l[0..3]); ref_cpu.cpp:28-31.
+__device__ inline int subblock_ls(uint32_t h0, uint32_t h1, int ib) {
+    const uint32_t lo = (h1 >> (4 * ib)) & 0xFu;
+    const uint32_t hi = (h0 >> (16 + 2 * ib)) & 0x3u;
+    return (int)(lo | (hi << 4));
+}
+
+// kvalues_iq4nl (kernels/common/block_iq4_xs.h:22-24) as four little-endian
+// byte quadruples: entries 0-3, 4-7, 8-11, 12-15.
+constexpr uint32_t KV0 = 0xBFAD9881u;  // -127 -104  -83  -65
+constexpr uint32_t KV1 = 0xF6EADDCFu;  //  -49  -35  -22  -10
+constexpr uint32_t KV2 = 0x26190D01u;  //    1   13   25   38
+constexpr uint32_t KV3 = 0x71594535u;  //   53   69   89  113
+
+// Eight 4-bit codes in one dword (byte i = codes 2i, 2i+1 as lo|hi<<4) ->
+// lo: 4 int8 codebook values of the low nibbles, hi: of the high nibbles.
+// v_perm_b32 selects bytes of {S0:S1}: selectors 0-3 pick S1, 4-7 pick S0, so
+// one perm looks up the 3 low index bits in half of the table and a third
+// perm chooses between the two halves with bit 3.
+__device__ inline void decode_codes(uint32_t q, uint32_t& lo, uint32_t& hi) {
+    const uint32_t ia = q & 0x07070707u;
+    const uint32_t ib = (q >> 4) & 0x07070707u;
+    const uint32_t la = __builtin_amdgcn_perm(KV1, KV0, ia);
+    const uint32_t ua = __builtin_amdgcn_perm(KV3, KV2, ia);
+    const uint32_t lb = __builtin_amdgcn_perm(KV1, KV0, ib);
+    const uint32_t ub = __builtin_amdgcn_perm(KV3, KV2, ib);
+    const uint32_t sa = ((q >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t sb = ((q >> 5) & 0x04040404u) | 0x03020100u;
+    lo = __builtin_amdgcn_perm(ua, la, sa);
+    hi = __builtin_amdgcn_perm(ub, lb, sb);
+}
+
+__device__ inline int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Integer dot of one 32-weight sub-block: 16 qs bytes (w) against the 32
+// Q8_1 codes of the matching activation block (a = bytes 0-15, b = 16-31).
+// Weight j (j<16) is the low nibble of qs byte j, weight j+16 its high nibble
+// (ref_cpu.cpp:35-46).
+__device__ inline int subblock_dot(const v4i& w, const v4i& a, const v4i& b) {
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t lo, hi;
+        decode_codes((uint32_t)w[j], lo, hi);
+        s = dot4(lo, (uint32_t)a[j], s);
+        s = dot4(hi, (uint32_t)b[j], s);
+    }
+    return s;
+}
+
+// Full-wave (64-lane) sum; every lane receives the total.
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace iq4xs

@@ -1,0 +1,39 @@
+// iq4xs_internal.h -- launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include "iq4xs_device.h"
+
+namespace iq4xs {
+
+// Activation / output layouts.
+constexpr int LAYOUT_KM = 0;  // X[k*M+m], Y[n*M+m]   (standalone API)
+constexpr int LAYOUT_MK = 1;  // X[m*K+k], Y[m*N+n]   (ggml src1 / dst)
+
+// Largest column count served by the streaming GEMV; wider batches go to the
+// MFMA GEMM.
+constexpr int GEMV_MAX_COLS = 8;
+
+hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds,
+                           block_q8_1* blocks, hipStream_t stream);
+hipError_t launch_planar_to_blocks(const int8_t* qs, const uint32_t* ds, int64_t K, int64_t M, block_q8_1* blocks,
+                                   hipStream_t stream);
+
+// y[c] = W x[c] for c < M <= GEMV_MAX_COLS on planar Q8_1 activations.
+// Output element (m, n) goes to Y[m*ldy_m + n*ldy_n].  dbg (optional) receives
+// the scaled int32 sum of every sub-block: dbg[(m*N + n)*(K/32) + kb].
+hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
+                       int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
+
+// Same contract on the int8 MFMA path (any M >= 1).
+hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
+                       int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
+
+// One v_mfma_i32_32x32x32_i8 on A[32][32], B[32][32] (k-contiguous rows) ->
+// C[32][32] = A B^T, through the operand layouts the GEMM uses.
+hipError_t launch_probe_mfma(const int8_t* A, const int8_t* B, int32_t* C, hipStream_t stream);
+
+hipError_t launch_fill_weights(uint8_t* W, int64_t n_blocks, uint64_t seed, int64_t first_block,
+                               hipStream_t stream);
+hipError_t launch_fill_activations(float* x, int64_t n, uint64_t seed, int outliers, hipStream_t stream);
+
+}  // namespace iq4xs

@@ -1,0 +1,133 @@
+// quantize_q8_1.hip -- fp32 activations -> Q8_1 on gfx950.
+//
+// Semantics: real_stock_dp4a_comparator.hip:230-264 (device quantiser) and
+// :278-306 (batched over columns).  Per 32-element block:
+//   amax = max|x|, sum = sum x (pairwise tree: x[t]+x[t+16], then +8, +4,
+//   +2, +1 -- the reference's xor butterfly seen from lane 0), d = amax/127
+//   (IEEE division), q = amax ? (int8)roundf(x/d) : 0, ds = rtz-half2(d, sum).
+//
+// MI355X mapping: one lane owns one whole block, so the tree is evaluated in
+// registers with no cross-lane traffic.  Lanes walk consecutive blocks of the
+// contiguous dimension so every load instruction is coalesced:
+//   layout MK (X[m*K+k], ggml src1 and bs=1 vectors): lane <-> block along k,
+//     each lane streams its 128 contiguous bytes;
+//   layout KM (X[k*M+m], standalone API): lane <-> column m, each of the 32
+//     loads of a wave covers 64 consecutive floats.
+#include "iq4xs_device.h"
+#include "iq4xs_internal.h"
+
+namespace iq4xs {
+
+__device__ inline void quantize_block_regs(const float (&x)[32], uint32_t (&q)[8], uint32_t& ds) {
+    float a[16], s[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        a[t] = fmaxf(fabsf(x[t]), fabsf(x[t + 16]));
+        s[t] = x[t] + x[t + 16];
+    }
+#pragma unroll
+    for (int w = 8; w > 0; w >>= 1) {
+#pragma unroll
+        for (int t = 0; t < w; ++t) {
+            a[t] = fmaxf(a[t], a[t + w]);
+            s[t] = s[t] + s[t + w];
+        }
+    }
+    const float amax = a[0];
+    const float d = amax / 127.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qi = (amax != 0.0f) ? (int)roundf(x[4 * j + i] / d) : 0;
+            packed |= ((uint32_t)qi & 0xFFu) << (8 * i);
+        }
+        q[j] = packed;
+    }
+    ds = float_to_half_bits_rtz(d) | (float_to_half_bits_rtz(s[0]) << 16);
+}
+
+template <int kLayout>
+__global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restrict__ X, int64_t K, int64_t M,
+                                                            int8_t* __restrict__ qs, uint32_t* __restrict__ ds,
+                                                            block_q8_1* __restrict__ blocks) {
+    const int64_t nb = K / QK8_1;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= nb * M) return;
+    int64_t m, ib;
+    float x[32];
+    if (kLayout == LAYOUT_MK) {
+        m = g / nb;
+        ib = g - m * nb;
+        const v4f* p = reinterpret_cast<const v4f*>(X + m * K + ib * QK8_1);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const v4f v = p[j];
+            x[4 * j + 0] = v.x;
+            x[4 * j + 1] = v.y;
+            x[4 * j + 2] = v.z;
+            x[4 * j + 3] = v.w;
+        }
+    } else {
+        ib = g / M;
+        m = g - ib * M;
+        const float* p = X + ib * QK8_1 * M + m;
+#pragma unroll
+        for (int t = 0; t < 32; ++t) x[t] = p[(int64_t)t * M];
+    }
+    uint32_t q[8], dsw;
+    quantize_block_regs(x, q, dsw);
+    if (qs != nullptr) {
+        v4i* o = reinterpret_cast<v4i*>(qs + m * K + ib * QK8_1);
+        o[0] = v4i{(int)q[0], (int)q[1], (int)q[2], (int)q[3]};
+        o[1] = v4i{(int)q[4], (int)q[5], (int)q[6], (int)q[7]};
+        ds[m * nb + ib] = dsw;
+    }
+    if (blocks != nullptr) {
+        uint32_t* o = reinterpret_cast<uint32_t*>(blocks + m * nb + ib);
+        o[0] = dsw;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[1 + j] = q[j];
+    }
+}
+
+// Planar workspace -> 36-byte ggml blocks (debug export for bit-exact checks).
+__global__ __launch_bounds__(256) void planar_to_blocks_kernel(const int8_t* __restrict__ qs,
+                                                               const uint32_t* __restrict__ ds, int64_t K, int64_t M,
+                                                               block_q8_1* __restrict__ blocks) {
+    const int64_t nb = K / QK8_1;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= nb * M) return;
+    const int64_t m = g / nb, ib = g - m * nb;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(qs + m * K + ib * QK8_1);
+    uint32_t* o = reinterpret_cast<uint32_t*>(blocks + g);
+    o[0] = ds[g];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[1 + j] = src[j];
+}
+
+hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds,
+                           block_q8_1* blocks, hipStream_t stream) {
+    const int64_t total = (K / QK8_1) * M;
+    const int64_t grid = (total + 255) / 256;
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    if (layout == LAYOUT_MK)
+        hipLaunchKernelGGL(quantize_q8_1_kernel<LAYOUT_MK>, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs,
+                           ds, blocks);
+    else
+        hipLaunchKernelGGL(quantize_q8_1_kernel<LAYOUT_KM>, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs,
+                           ds, blocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_planar_to_blocks(const int8_t* qs, const uint32_t* ds, int64_t K, int64_t M, block_q8_1* blocks,
+                                   hipStream_t stream) {
+    const int64_t total = (K / QK8_1) * M;
+    const int64_t grid = (total + 255) / 256;
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(planar_to_blocks_kernel, dim3((unsigned)grid), dim3(256), 0, stream, qs, ds, K, M, blocks);
+    return hipGetLastError();
+}
+
+}  // namespace iq4xs

@@ -1,0 +1,278 @@
+"""GPU parity tests: every call goes through the C ABI of libiq4xs_mi355x.so
+and is compared with the CPU oracle on the same seeded inputs.
+
+Bars (from the path's contract):
+  * Q8_1 blocks and per-32-element int32 sub-block sums: bit-exact;
+  * fp32 outputs: relative L2 <= 1e-4 against the reference kernel semantics
+    (oracle gemv/gemm_semantics), cosine >= 0.99999 against the FP64 oracle
+    evaluated on the dequantised Q8_1 activations x_hat.
+"""
+import numpy as np
+import pytest
+
+from oracle.oracle import BLOCK_Q8_1, LAYOUT_KM, LAYOUT_MK, compute_metrics
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+REL_L2_TOL = 1e-4
+COS_TOL = 0.99999
+
+CONFIG1 = {  # K -> N of the 27B-class decode projections
+    "q_proj": (5120, 8192), "k_proj": (5120, 1024), "v_proj": (5120, 1024), "o_proj": (8192, 5120),
+    "gate_proj": (5120, 17408), "up_proj": (5120, 17408), "down_proj": (17408, 5120),
+}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    torch.cuda.set_device(0)
+    return torch.device("cuda:0")
+
+
+def D(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def check_outputs(orc, W, AQ, Y_gpu_mn, K, N, M, label):
+    """Y_gpu_mn: numpy [M, N]."""
+    Y_sem = orc.gemm_semantics(W, AQ, K, N, M).T
+    m = compute_metrics(Y_sem, Y_gpu_mn)
+    assert m["rel_l2"] <= REL_L2_TOL and not m["bad"], (label, m)
+    xhat = orc.dequant_q8_1(AQ).reshape(M, K)
+    Y64 = orc.gemm_fp64(W, np.ascontiguousarray(xhat.T), K, N, M, nthreads=8).T
+    m64 = compute_metrics(Y64, Y_gpu_mn)
+    assert m64["cosine"] >= COS_TOL, (label, m64)
+    return m, m64
+
+
+# ------------------------------------------------------------------ building blocks
+def test_probe_mfma_layout(pkg, dev):
+    rng = np.random.default_rng(0)
+    A = rng.integers(-128, 128, (32, 32), dtype=np.int8)
+    B = rng.integers(-128, 128, (32, 32), dtype=np.int8)
+    C = torch.zeros((32, 32), dtype=torch.int32, device=dev)
+    pkg.lib().check("iq4xs_probe_mfma_i8", D(A, dev).data_ptr(), D(B, dev).data_ptr(), C.data_ptr(), stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(C.cpu().numpy(), A.astype(np.int32) @ B.astype(np.int32).T)
+
+
+def test_synthetic_weights_match_oracle(pkg, orc, dev):
+    W = pkg.synthetic_weights(4096, 48, seed=42, device=dev).cpu().numpy()
+    assert np.array_equal(W, orc.gen_weights(4096, 48, seed=42))
+    part = pkg.synthetic_weights(256, 7, seed=42, first_block=123, device=dev).cpu().numpy()
+    assert np.array_equal(part, W[123 * 136:130 * 136])
+
+
+def test_synthetic_activations_distribution(pkg, dev):
+    x = pkg.synthetic_activations(1 << 20, seed=5, device=dev).cpu().numpy()
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
+    xo = pkg.synthetic_activations(1 << 20, seed=5, outliers=True, device=dev).cpu().numpy()
+    assert 0.008 < np.mean(xo != x) < 0.012
+
+
+@pytest.mark.parametrize("K,M,layout,outliers", [
+    (256, 1, LAYOUT_MK, False), (5120, 1, LAYOUT_MK, False), (17408, 1, LAYOUT_MK, True),
+    (5120, 8, LAYOUT_MK, True), (1024, 37, LAYOUT_KM, False), (2048, 512, LAYOUT_MK, True),
+    (512, 300, LAYOUT_KM, True)])
+def test_q8_1_blocks_bit_exact(pkg, orc, dev, K, M, layout, outliers):
+    X = orc.gen_activations(K * M, seed=K + M, outliers=outliers)
+    X = X.reshape(M, K) if layout == LAYOUT_MK else X.reshape(K, M)
+    ref = orc.quantize_q8_1_batched(X, K, M, layout)
+    ws = pkg.quantize_q8_1(D(X, dev), K, M, layout)
+    got = pkg.q8_1_blocks(ws, K, M).cpu().numpy().ravel()
+    assert np.array_equal(got, ref)
+
+
+def test_q8_1_reference_entry_points(pkg, orc, dev):
+    L = pkg.lib()
+    K, M = 1024, 6
+    x = orc.gen_activations(K, seed=1, outliers=True)
+    y = torch.zeros(K // 32 * 36, dtype=torch.uint8, device=dev)
+    L.check("quantize_row_q8_1_gpu", D(x, dev).data_ptr(), y.data_ptr(), K, stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), orc.quantize_q8_1(x))
+    X = orc.gen_activations(K * M, seed=2).reshape(K, M)
+    Y = torch.zeros(M * K // 32 * 36, dtype=torch.uint8, device=dev)
+    L.check("quantize_row_q8_1_batched_gpu", D(X, dev).data_ptr(), Y.data_ptr(), K, M, stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(Y.cpu().numpy(), orc.quantize_q8_1_batched(X, K, M, LAYOUT_KM))
+
+
+def test_q8_1_special_blocks(pkg, orc, dev):
+    blocks = []
+    blocks.append(np.zeros(32, np.float32))                                   # all zero
+    b = np.zeros(32, np.float32); b[5] = 3.0; blocks.append(b)                # single nonzero
+    b = np.zeros(32, np.float32); b[0] = 127.0
+    b[1:9] = [2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 3.5, 126.5]; blocks.append(b)  # exact .5 ties
+    b = np.zeros(32, np.float32); b[0] = 2.0**24; b[16] = -(2.0**24 - 1); b[1] = 0.75; blocks.append(b)  # tree order
+    b = np.zeros(32, np.float32); b[0] = 1.0; b[1] = -0.0; blocks.append(b)   # -0.0
+    b = np.full(32, 1e-30, np.float32); blocks.append(b)                      # d underflows fp16
+    b = np.full(32, -7e4, np.float32); blocks.append(b)                       # sum overflows fp16
+    x = np.concatenate(blocks + [np.zeros(32 * (8 - len(blocks)), np.float32)])
+    ws = pkg.quantize_q8_1(D(x, dev), 256, 1, LAYOUT_MK)
+    got = pkg.q8_1_blocks(ws, 256, 1).cpu().numpy().ravel()
+    assert np.array_equal(got, orc.quantize_q8_1(x))
+
+
+# ------------------------------------------------------------------ GEMV / GEMM kernels
+GEMV_CASES = [(256, 1, 1), (768, 7, 1), (1024, 64, 1), (5120, 333, 1), (4096, 4096, 1),
+              (768, 9, 2), (1280, 65, 3), (2048, 130, 4), (256, 5, 5), (5120, 100, 6), (512, 77, 7),
+              (8192, 96, 8), (17408, 40, 8)]
+
+
+@pytest.mark.parametrize("K,N,M", GEMV_CASES)
+def test_gemv_sums_and_outputs(pkg, orc, dev, K, N, M):
+    W = orc.gen_weights(K, N, seed=1000 + K + N)
+    X = orc.gen_activations(K * M, seed=2000 + M, outliers=(M > 1)).reshape(M, K)
+    AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
+    Wd = D(W, dev)
+    ws = pkg.quantize_q8_1(D(X, dev), K, M, LAYOUT_MK)
+    S, Y = pkg.subblock_sums(Wd, ws, K, N, M, pkg.PATH_GEMV)
+    Y2 = pkg.mul_mat_q8_1(Wd, ws, K, N, M, LAYOUT_MK, pkg.PATH_GEMV)
+    torch.cuda.synchronize()
+    assert np.array_equal(S.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, M))
+    check_outputs(orc, W, AQ, Y.cpu().numpy(), K, N, M, "gemv+dbg")
+    assert torch.equal(Y, Y2)  # the debug store does not change the arithmetic
+
+
+GEMM_CASES = [(256, 64, 64), (256, 1, 1), (512, 100, 20), (768, 130, 65), (1024, 64, 128),
+              (2048, 200, 100), (512, 64, 512), (256, 300, 9)]
+
+
+@pytest.mark.parametrize("K,N,M", GEMM_CASES)
+def test_gemm_sums_and_outputs(pkg, orc, dev, K, N, M):
+    W = orc.gen_weights(K, N, seed=3000 + K + N)
+    X = orc.gen_activations(K * M, seed=4000 + M, outliers=True).reshape(M, K)
+    AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
+    Wd = D(W, dev)
+    ws = pkg.quantize_q8_1(D(X, dev), K, M, LAYOUT_MK)
+    S, Y = pkg.subblock_sums(Wd, ws, K, N, M, pkg.PATH_GEMM)
+    Y2 = pkg.mul_mat_q8_1(Wd, ws, K, N, M, LAYOUT_MK, pkg.PATH_GEMM)
+    Ykm = pkg.mul_mat_q8_1(Wd, ws, K, N, M, LAYOUT_KM, pkg.PATH_GEMM)
+    torch.cuda.synchronize()
+    assert np.array_equal(S.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, M))
+    check_outputs(orc, W, AQ, Y.cpu().numpy(), K, N, M, "gemm+dbg")
+    assert torch.equal(Y, Y2)
+    assert torch.equal(Ykm.T, Y2)
+
+
+def test_gemv_and_gemm_paths_agree(pkg, orc, dev):
+    K, N, M = 2048, 256, 8
+    W = D(orc.gen_weights(K, N, seed=5), dev)
+    X = D(orc.gen_activations(K * M, seed=6).reshape(M, K), dev)
+    ws = pkg.quantize_q8_1(X, K, M)
+    S1, Y1 = pkg.subblock_sums(W, ws, K, N, M, pkg.PATH_GEMV)
+    S2, Y2 = pkg.subblock_sums(W, ws, K, N, M, pkg.PATH_GEMM)
+    torch.cuda.synchronize()
+    assert torch.equal(S1, S2)
+    assert compute_metrics(Y1.cpu().numpy(), Y2.cpu().numpy())["rel_l2"] < 1e-6
+
+
+# ------------------------------------------------------------------ reference entry points
+def test_reference_entry_points(pkg, orc, dev):
+    L = pkg.lib()
+    K, N = 5120, 160
+    W = orc.gen_weights(K, N, seed=77)
+    x = orc.gen_activations(K, seed=78)
+    AQ = orc.quantize_q8_1(x)
+    y_sem = orc.gemv_semantics(W, AQ, K, N)
+    Wd, xd = D(W, dev), D(x, dev)
+    for fn in ("gemv_iq4xs_stock_dp4a_gpu", "gemv_iq4xs_dp4a_coop_gpu", "custom_gemv_iq4xs_dispatch"):
+        y = torch.full((N,), float("nan"), device=dev)
+        L.check(fn, Wd.data_ptr(), xd.data_ptr(), y.data_ptr(), K, N, stream())
+        torch.cuda.synchronize()
+        assert compute_metrics(y_sem, y.cpu().numpy())["rel_l2"] <= REL_L2_TOL, fn
+    # standalone GEMM: X[k*M+m] -> Y[n*M+m] (real_stock_dp4a_comparator.hip:505-512)
+    for M in (4, 96):
+        X_km = orc.gen_activations(K * M, seed=79 + M).reshape(K, M)
+        AQm = orc.quantize_q8_1_batched(X_km, K, M, LAYOUT_KM)
+        Y_sem = orc.gemm_semantics(W, AQm, K, N, M)          # [N, M]
+        Y = torch.full((N, M), float("nan"), device=dev)
+        L.check("gemm_iq4xs_stock_dp4a_gpu", Wd.data_ptr(), D(X_km, dev).data_ptr(), Y.data_ptr(), K, N, M, stream())
+        # ggml: X[m*K+k] -> Y[m*N+n] (patch:117,129)
+        Yg = torch.full((M, N), float("nan"), device=dev)
+        L.check("custom_gemm_iq4xs_dispatch", Wd.data_ptr(), D(X_km.T, dev).data_ptr(), Yg.data_ptr(), K, N, M,
+                stream())
+        torch.cuda.synchronize()
+        assert compute_metrics(Y_sem, Y.cpu().numpy())["rel_l2"] <= REL_L2_TOL
+        assert compute_metrics(Y_sem.T, Yg.cpu().numpy())["rel_l2"] <= REL_L2_TOL
+
+
+def test_invalid_arguments_on_gpu(pkg, dev):
+    L = pkg.lib()
+    W = torch.zeros(136 * 4, dtype=torch.uint8, device=dev)
+    x = torch.zeros(256, device=dev)
+    y = torch.zeros(4, device=dev)
+    assert L.gemv_iq4xs_stock_dp4a_gpu(W.data_ptr(), x.data_ptr(), y.data_ptr(), 255, 4, stream()) == 1
+    assert L.iq4xs_mul_mat_q8_1(W.data_ptr(), x.data_ptr() + 4, y.data_ptr(), 256, 4, 1, LAYOUT_MK, -1,
+                                stream()) == 1  # misaligned workspace
+    assert L.iq4xs_mul_mat_q8_1(W.data_ptr(), x.data_ptr(), y.data_ptr(), 256, 4, 9, LAYOUT_MK, pkg.PATH_GEMV,
+                                stream()) == 1  # GEMV serves at most 8 columns
+
+
+# ------------------------------------------------------------------ full-size shapes
+@pytest.mark.parametrize("proj", list(CONFIG1))
+def test_config1_gemv_bs1_full_size(pkg, orc, dev, proj):
+    K, N = CONFIG1[proj]
+    W = pkg.synthetic_weights(K, N, seed=42, device=dev)
+    x = orc.gen_activations(K, seed=43)
+    y = pkg.mul_mat(W, D(x, dev), K, N, 1)
+    torch.cuda.synchronize()
+    Wh = W.cpu().numpy()
+    AQ = orc.quantize_q8_1(x)
+    y_sem = orc.gemv_semantics(Wh, AQ, K, N)
+    m = compute_metrics(y_sem, y.cpu().numpy().ravel())
+    assert m["rel_l2"] <= REL_L2_TOL, m
+    y_hat = orc.gemv_fp64(Wh, orc.dequant_q8_1(AQ), K, N)
+    assert compute_metrics(y_hat, y.cpu().numpy().ravel())["cosine"] >= COS_TOL
+
+
+@pytest.mark.parametrize("proj,M", [("q_proj", 2), ("o_proj", 4), ("down_proj", 8), ("gate_proj", 8)])
+def test_config2_small_batch_full_size(pkg, orc, dev, proj, M):
+    K, N = CONFIG1[proj]
+    W = pkg.synthetic_weights(K, N, seed=44, device=dev)
+    X = orc.gen_activations(K * M, seed=45, outliers=True).reshape(M, K)
+    Y = pkg.mul_mat(W, D(X, dev), K, N, M)
+    torch.cuda.synchronize()
+    Wh = W.cpu().numpy()
+    AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
+    rows = np.random.default_rng(M).choice(N, 256, replace=False)
+    Wsub = Wh.reshape(N, -1)[rows].ravel()
+    Y_sem = orc.gemm_semantics(Wsub, AQ, K, len(rows), M).T
+    m = compute_metrics(Y_sem, Y.cpu().numpy()[:, rows])
+    assert m["rel_l2"] <= REL_L2_TOL, m
+
+
+@pytest.mark.parametrize("proj,M", [("q_proj", 512), ("down_proj", 512), ("o_proj", 2048)])
+def test_config3_prefill_gemm_sampled_rows(pkg, orc, dev, proj, M):
+    K, N = CONFIG1[proj]
+    W = pkg.synthetic_weights(K, N, seed=46, device=dev)
+    X = pkg.synthetic_activations(K * M, seed=47, device=dev)
+    ws = pkg.quantize_q8_1(X, K, M)
+    Y = pkg.mul_mat_q8_1(W, ws, K, N, M)
+    torch.cuda.synchronize()
+    AQ = pkg.q8_1_blocks(ws, K, M).cpu().numpy().ravel()
+    assert np.array_equal(AQ, orc.quantize_q8_1_batched(X.cpu().numpy(), K, M, LAYOUT_MK))
+    rows = np.sort(np.random.default_rng(M).choice(N, 12, replace=False))
+    Wsub = W.cpu().numpy().reshape(N, -1)[rows].ravel()
+    Y_sem = orc.gemm_semantics(Wsub, AQ, K, len(rows), M).T
+    m = compute_metrics(Y_sem, Y.cpu().numpy()[:, rows])
+    assert m["rel_l2"] <= REL_L2_TOL, m
+
+
+def test_deterministic_replay(pkg, dev):
+    K, N, M = 5120, 1024, 64
+    W = pkg.synthetic_weights(K, N, seed=1, device=dev)
+    X = pkg.synthetic_activations(K * M, seed=2, device=dev)
+    a = pkg.mul_mat(W, X, K, N, M)
+    b = pkg.mul_mat(W, X, K, N, M)
+    c = pkg.mul_mat(W, X[:K], K, N, 1)
+    d = pkg.mul_mat(W, X[:K], K, N, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d)
