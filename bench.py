@@ -74,7 +74,7 @@ def cpu_baseline(seconds: float) -> dict:
             done_bytes += gemv_bytes(K, N)
         passes += 1
         el = time.perf_counter() - t0
-        if el >= seconds or passes >= 8:
+        if el >= seconds:
             break
     cpu = "unknown"
     try:

@@ -7,7 +7,8 @@
 //
 // MI355X mapping.  A workgroup (4 waves) owns a 64-row x 64-token output
 // tile and walks K one 256-weight super-block at a time:
-//   1. the 64 weight rows' super-blocks are decoded (v_perm codebook lookup)
+//   1. the 64 weight rows' super-blocks are decoded (v_perm codebook lookup,
+//      decode_codes_x)
 //      straight into int8 LDS tiles, the per-sub-block weight scales
 //      d*(ls-32) into a float table;
 //   2. the 64 tokens' Q8_1 codes are copied to LDS, their d into a table;
@@ -44,6 +45,7 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
     __shared__ __attribute__((aligned(16))) int8_t sX[GEMM_BM * 256];
     __shared__ __attribute__((aligned(16))) float sA[8][GEMM_BN];
     __shared__ __attribute__((aligned(16))) float sB[8][GEMM_BM];
+    __shared__ int sL[kDebug ? 8 : 1][GEMM_BN];  // ls - 32, only for the debug export
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -70,10 +72,11 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
             const v4i w = *reinterpret_cast<const v4i_a8*>(blk + 8 + 16 * s);
             uint32_t lo[4], hi[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) decode_codes((uint32_t)w[j], lo[j], hi[j]);
+            for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)w[j], lo[j], hi[j]);
             *reinterpret_cast<v4i*>(sW + lds_swz(r, 2 * s)) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
             *reinterpret_cast<v4i*>(sW + lds_swz(r, 2 * s + 1)) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
             sA[s][r] = half_bits_to_float(h.x & 0xFFFFu) * (float)(subblock_ls(h.x, h.y, s) - 32);
+            if (kDebug) sL[s][r] = subblock_ls(h.x, h.y, s) - 32;
         }
         // 2. activations: 64 tokens x 16 chunks of 16 codes, four per thread
 #pragma unroll
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
                 acc[e] += (sA[s][i] * bx) * (float)c[e];
                 if (kDebug) {
                     const int64_t n = n0 + i, m = m0 + rb;
-                    if (n < N && m < M) dbg[(m * N + n) * nb + kb * 8 + s] = c[e];
+                    if (n < N && m < M) dbg[(m * N + n) * nb + kb * 8 + s] = c[e] * sL[s][i];
                 }
             }
         }

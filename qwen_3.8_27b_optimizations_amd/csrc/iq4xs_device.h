@@ -112,6 +112,41 @@ __device__ inline int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// Cheaper exact decode through the v_perm_b32 selector "specials": selector
+// bytes 8-11 return 0x00/0xFF from the sign bit of table byte 1/3/5/7, 12
+// returns 0x00 and 13-15 return 0xFF.  With the raw 4-bit code n as the
+// selector of table A and n^8 as the selector of table B, exactly one lookup
+// hits its table and the other yields a known special byte; the tables below
+// are the (unique) pair for which A(n) ^ B(n^8) == kvalues_iq4nl[n] for all n.
+// Five index ops + four perms + two xors decode eight codes (vs thirteen ops
+// with the two-level lookup above).
+constexpr uint32_t KXA0 = 0x40529881u, KXA1 = 0x091522cfu;
+constexpr uint32_t KXB0 = 0x26190dfeu, KXB1 = 0x8ea6ba35u;
+
+__device__ inline void decode_codes_x(uint32_t q, uint32_t& lo, uint32_t& hi) {
+    const uint32_t nl = q & 0x0F0F0F0Fu;
+    const uint32_t xl = (q ^ 0x08080808u) & 0x0F0F0F0Fu;
+    const uint32_t t = q >> 4;
+    const uint32_t nh = t & 0x0F0F0F0Fu;
+    const uint32_t xh = (t ^ 0x08080808u) & 0x0F0F0F0Fu;
+    lo = __builtin_amdgcn_perm(KXA1, KXA0, nl) ^ __builtin_amdgcn_perm(KXB1, KXB0, xl);
+    hi = __builtin_amdgcn_perm(KXA1, KXA0, nh) ^ __builtin_amdgcn_perm(KXB1, KXB0, xh);
+}
+
+// fp32 sum over the 64 lanes of a wave (DPP inside rows of 16, then one
+// readlane per row); the result is wave-uniform.
+__device__ inline float wave_sum_dpp(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 // Integer dot of one 32-weight sub-block: 16 qs bytes (w) against the 32
 // Q8_1 codes of the matching activation block (a = bytes 0-15, b = 16-31).
 // Weight j (j<16) is the low nibble of qs byte j, weight j+16 its high nibble

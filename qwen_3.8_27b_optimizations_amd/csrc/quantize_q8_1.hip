@@ -6,13 +6,13 @@
 //   +2, +1 -- the reference's xor butterfly seen from lane 0), d = amax/127
 //   (IEEE division), q = amax ? (int8)roundf(x/d) : 0, ds = rtz-half2(d, sum).
 //
-// MI355X mapping: one lane owns one whole block, so the tree is evaluated in
-// registers with no cross-lane traffic.  Lanes walk consecutive blocks of the
-// contiguous dimension so every load instruction is coalesced:
-//   layout MK (X[m*K+k], ggml src1 and bs=1 vectors): lane <-> block along k,
-//     each lane streams its 128 contiguous bytes;
-//   layout KM (X[k*M+m], standalone API): lane <-> column m, each of the 32
-//     loads of a wave covers 64 consecutive floats.
+// MI355X mapping:
+//   layout MK (X[m*K+k], ggml src1 and bs=1 vectors): eight lanes per block,
+//     four elements and four divisions per lane, tree finished with
+//     ds_swizzle xor steps (quantize_q8_1_rows_kernel);
+//   layout KM (X[k*M+m], standalone API): one lane per block, lanes walk
+//     consecutive columns m so each of the 32 loads of a wave covers 64
+//     consecutive floats; the tree is evaluated in registers.
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 
@@ -107,17 +107,76 @@ __global__ __launch_bounds__(256) void planar_to_blocks_kernel(const int8_t* __r
     for (int j = 0; j < 8; ++j) o[1 + j] = src[j];
 }
 
+// Row-contiguous layout (ggml src1, bs=1 vectors): eight lanes per block,
+// lane j holds x[j], x[j+8], x[j+16], x[j+24].  The reference tree is kept
+// exactly: x[t]+x[t+16] and the +8 level inside the lane, then xor-swizzles
+// 4, 2, 1 across the eight lanes (ds_swizzle in bitmask mode never crosses a
+// 32-lane half, and whole 8-lane groups are always active together).
+template <int X>
+__device__ inline float swizzle_xor(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (X << 10)));
+}
+
+__global__ __launch_bounds__(256) void quantize_q8_1_rows_kernel(const float* __restrict__ X, int64_t K, int64_t M,
+                                                                 int8_t* __restrict__ qs, uint32_t* __restrict__ ds,
+                                                                 block_q8_1* __restrict__ blocks) {
+    const int64_t nb = K / QK8_1;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t blk = t >> 3;
+    if (blk >= nb * M) return;  // whole 8-lane groups
+    const int j = (int)(t & 7);
+    const int64_t m = blk / nb, ib = blk - m * nb;
+    const float* p = X + m * K + ib * QK8_1 + j;
+    const float x0 = p[0], x1 = p[8], x2 = p[16], x3 = p[24];
+    float a = fmaxf(fmaxf(fabsf(x0), fabsf(x2)), fmaxf(fabsf(x1), fabsf(x3)));
+    float s = (x0 + x2) + (x1 + x3);
+    a = fmaxf(a, swizzle_xor<4>(a));
+    s = s + swizzle_xor<4>(s);
+    a = fmaxf(a, swizzle_xor<2>(a));
+    s = s + swizzle_xor<2>(s);
+    a = fmaxf(a, swizzle_xor<1>(a));
+    s = s + swizzle_xor<1>(s);
+    const float d = a / 127.0f;
+    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    if (a != 0.0f) {
+        q0 = (int)roundf(x0 / d);
+        q1 = (int)roundf(x1 / d);
+        q2 = (int)roundf(x2 / d);
+        q3 = (int)roundf(x3 / d);
+    }
+    const uint32_t dsw = float_to_half_bits_rtz(d) | (float_to_half_bits_rtz(s) << 16);
+    if (qs != nullptr) {
+        int8_t* o = qs + m * K + ib * QK8_1 + j;
+        o[0] = (int8_t)q0;
+        o[8] = (int8_t)q1;
+        o[16] = (int8_t)q2;
+        o[24] = (int8_t)q3;
+        if (j == 0) ds[blk] = dsw;
+    }
+    if (blocks != nullptr) {
+        int8_t* o = blocks[blk].qs + j;
+        o[0] = (int8_t)q0;
+        o[8] = (int8_t)q1;
+        o[16] = (int8_t)q2;
+        o[24] = (int8_t)q3;
+        if (j == 0) blocks[blk].ds = dsw;
+    }
+}
+
 hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds,
                            block_q8_1* blocks, hipStream_t stream) {
     const int64_t total = (K / QK8_1) * M;
+    if (layout == LAYOUT_MK) {
+        const int64_t grid = (total * 8 + 255) / 256;
+        if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        hipLaunchKernelGGL(quantize_q8_1_rows_kernel, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs, ds,
+                           blocks);
+        return hipGetLastError();
+    }
     const int64_t grid = (total + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-    if (layout == LAYOUT_MK)
-        hipLaunchKernelGGL(quantize_q8_1_kernel<LAYOUT_MK>, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs,
-                           ds, blocks);
-    else
-        hipLaunchKernelGGL(quantize_q8_1_kernel<LAYOUT_KM>, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs,
-                           ds, blocks);
+    hipLaunchKernelGGL(quantize_q8_1_kernel<LAYOUT_KM>, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs, ds,
+                       blocks);
     return hipGetLastError();
 }
 

@@ -57,7 +57,8 @@ def test_probe_mfma_layout(pkg, dev):
     A = rng.integers(-128, 128, (32, 32), dtype=np.int8)
     B = rng.integers(-128, 128, (32, 32), dtype=np.int8)
     C = torch.zeros((32, 32), dtype=torch.int32, device=dev)
-    pkg.lib().check("iq4xs_probe_mfma_i8", D(A, dev).data_ptr(), D(B, dev).data_ptr(), C.data_ptr(), stream())
+    Ad, Bd = D(A, dev), D(B, dev)  # keep both alive until the kernel has run
+    pkg.lib().check("iq4xs_probe_mfma_i8", Ad.data_ptr(), Bd.data_ptr(), C.data_ptr(), stream())
     torch.cuda.synchronize()
     assert np.array_equal(C.cpu().numpy(), A.astype(np.int32) @ B.astype(np.int32).T)
 
@@ -94,12 +95,14 @@ def test_q8_1_reference_entry_points(pkg, orc, dev):
     K, M = 1024, 6
     x = orc.gen_activations(K, seed=1, outliers=True)
     y = torch.zeros(K // 32 * 36, dtype=torch.uint8, device=dev)
-    L.check("quantize_row_q8_1_gpu", D(x, dev).data_ptr(), y.data_ptr(), K, stream())
+    xd = D(x, dev)
+    L.check("quantize_row_q8_1_gpu", xd.data_ptr(), y.data_ptr(), K, stream())
     torch.cuda.synchronize()
     assert np.array_equal(y.cpu().numpy(), orc.quantize_q8_1(x))
     X = orc.gen_activations(K * M, seed=2).reshape(K, M)
     Y = torch.zeros(M * K // 32 * 36, dtype=torch.uint8, device=dev)
-    L.check("quantize_row_q8_1_batched_gpu", D(X, dev).data_ptr(), Y.data_ptr(), K, M, stream())
+    Xd = D(X, dev)
+    L.check("quantize_row_q8_1_batched_gpu", Xd.data_ptr(), Y.data_ptr(), K, M, stream())
     torch.cuda.synchronize()
     assert np.array_equal(Y.cpu().numpy(), orc.quantize_q8_1_batched(X, K, M, LAYOUT_KM))
 
@@ -194,10 +197,11 @@ def test_reference_entry_points(pkg, orc, dev):
         AQm = orc.quantize_q8_1_batched(X_km, K, M, LAYOUT_KM)
         Y_sem = orc.gemm_semantics(W, AQm, K, N, M)          # [N, M]
         Y = torch.full((N, M), float("nan"), device=dev)
-        L.check("gemm_iq4xs_stock_dp4a_gpu", Wd.data_ptr(), D(X_km, dev).data_ptr(), Y.data_ptr(), K, N, M, stream())
+        Xkm_d, Xmk_d = D(X_km, dev), D(X_km.T, dev)
+        L.check("gemm_iq4xs_stock_dp4a_gpu", Wd.data_ptr(), Xkm_d.data_ptr(), Y.data_ptr(), K, N, M, stream())
         # ggml: X[m*K+k] -> Y[m*N+n] (patch:117,129)
         Yg = torch.full((M, N), float("nan"), device=dev)
-        L.check("custom_gemm_iq4xs_dispatch", Wd.data_ptr(), D(X_km.T, dev).data_ptr(), Yg.data_ptr(), K, N, M,
+        L.check("custom_gemm_iq4xs_dispatch", Wd.data_ptr(), Xmk_d.data_ptr(), Yg.data_ptr(), K, N, M,
                 stream())
         torch.cuda.synchronize()
         assert compute_metrics(Y_sem, Y.cpu().numpy())["rel_l2"] <= REL_L2_TOL
