@@ -126,6 +126,15 @@ int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64
 int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
                   size_t ws_bytes, void* stream);
 
+/* Small-batch (1 <= M <= 8) multiply that quantises X to Q8_1 inside the GEMV
+ * kernel (one launch, no workspace).  Same Q8_1 codes and sums as
+ * iq4xs_quantize_q8_1 + iq4xs_mul_mat_q8_1.  Returns IQ4XS_ERROR_NOT_SUPPORTED
+ * when M*K does not fit the kernel's on-chip activation buffer; the caller then
+ * uses the two-step path.  S (may be NULL) receives the per-sub-block int32
+ * sums exactly as iq4xs_subblock_sums lays them out. */
+int iq4xs_mul_mat_fused(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                        int32_t* S, void* stream);
+
 /* ================================ debug exports ================================
  * No counterpart in the reference; they exist so the Q8_1 blocks and the
  * per-32-element int32 sums can be checked bit for bit. */

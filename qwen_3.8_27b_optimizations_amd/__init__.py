@@ -56,6 +56,7 @@ SIGNATURES = {
     "iq4xs_quantize_q8_1": (_INT, [_P, _I64, _I64, _INT, _P, ctypes.c_size_t, _P]),
     "iq4xs_mul_mat_q8_1": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _INT, _P]),
     "iq4xs_mul_mat": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, ctypes.c_size_t, _P]),
+    "iq4xs_mul_mat_fused": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, _P]),
     "iq4xs_q8_1_to_blocks": (_INT, [_P, _P, _I64, _I64, _P]),
     "iq4xs_subblock_sums": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "iq4xs_probe_mfma_i8": (_INT, [_P, _P, _P, _P]),
@@ -168,6 +169,22 @@ def mul_mat(W, X, K: int, N: int, M: int, layout: int = LAYOUT_MK, ws=None, out=
     lib().check("iq4xs_mul_mat", W.data_ptr(), X.data_ptr(), out.data_ptr(), K, N, M, layout, ws.data_ptr(),
                 ws.numel(), _stream(torch))
     return out
+
+
+def mul_mat_fused(W, X, K: int, N: int, M: int, layout: int = LAYOUT_MK, out=None, sums: bool = False):
+    """Y = W * X for M <= 8 with the Q8_1 quantisation inside the GEMV kernel.
+
+    Raises Iq4xsError with code ERROR_NOT_SUPPORTED when M*K is too large for
+    the fused kernel.  With sums=True also returns S[M, N, K/32] (int32)."""
+    torch = _torch()
+    _check_weights(W, K, N)
+    if out is None:
+        shape = (M, N) if layout == LAYOUT_MK else (N, M)
+        out = torch.empty(shape, dtype=torch.float32, device=W.device)
+    S = torch.empty((M, N, K // QK8_1), dtype=torch.int32, device=W.device) if sums else None
+    lib().check("iq4xs_mul_mat_fused", W.data_ptr(), X.data_ptr(), out.data_ptr(), K, N, M, layout,
+                S.data_ptr() if sums else None, _stream(torch))
+    return (out, S) if sums else out
 
 
 def subblock_sums(W, ws, K: int, N: int, M: int, path: int):

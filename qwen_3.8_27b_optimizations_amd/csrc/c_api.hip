@@ -160,6 +160,18 @@ int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N,
                           as_stream(stream));
 }
 
+int iq4xs_mul_mat_fused(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                        int32_t* S, void* stream) {
+    if (!valid_mat(W, X, Y, K, N, M) || (layout != LAYOUT_KM && layout != LAYOUT_MK)) return hipErrorInvalidValue;
+    if (M > GEMV_MAX_COLS) return hipErrorNotSupported;
+    const int64_t ldy_m = (layout == LAYOUT_MK) ? N : 1;
+    const int64_t ldy_n = (layout == LAYOUT_MK) ? 1 : M;
+    const int64_t sc = (layout == LAYOUT_MK) ? K : 1;
+    const int64_t sk = (layout == LAYOUT_MK) ? 1 : M;
+    return launch_gemv_fused(static_cast<const uint8_t*>(W), X, sc, sk, Y, K, N, M, ldy_m, ldy_n, S,
+                             as_stream(stream));
+}
+
 int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, void* stream) {
     if (!ws || !blocks || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
     const Planar p = planar_view(ws, K, M);

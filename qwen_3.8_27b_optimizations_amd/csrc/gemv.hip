@@ -29,6 +29,7 @@
 // read through L1/L2.
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
+#include "q8_1_block.h"
 
 namespace iq4xs {
 
@@ -164,11 +165,33 @@ __device__ inline void stage_activations(const int8_t* __restrict__ aqs, const u
     for (int i = tid; i < nbs; i += nthreads) sdx[i] = half_bits_to_float(ads[i] & 0xFFFFu);
 }
 
-template <int C, int IR, bool kDebug>
+// Fused prologue: quantise the fp32 activations (element (c, k) at
+// X[c*sc + k*sk]) straight into LDS, eight lanes per block.  Only d is kept:
+// the dot uses the fp16-truncated d exactly as the planar path does.
+__device__ inline void quantize_to_lds(const float* __restrict__ X, int64_t sc, int64_t sk, int C, int K, int8_t* sq,
+                                       float* sdx, int tid, int nthreads) {
+    const int nb = K / QK8_1;
+    const int tasks = C * nb * 8;  // nthreads is a multiple of 64: 8-lane groups stay whole
+    for (int t = tid; t < tasks; t += nthreads) {
+        const int blk = t >> 3, j = t & 7;
+        const int cc = blk / nb, ib = blk - cc * nb;
+        const float* p = X + cc * sc + (int64_t)(ib * QK8_1 + j) * sk;
+        const Q8Block8 b = quantize_block8(p[0], p[8 * sk], p[16 * sk], p[24 * sk]);
+        int8_t* o = sq + cc * K + ib * QK8_1 + j;
+        o[0] = (int8_t)b.q0;
+        o[8] = (int8_t)b.q1;
+        o[16] = (int8_t)b.q2;
+        o[24] = (int8_t)b.q3;
+        if (j == 0) sdx[blk] = half_bits_to_float(b.ds & 0xFFFFu);
+    }
+}
+
+template <int C, int IR, bool kDebug, bool kFuse>
 __global__ __launch_bounds__(512) void gemv_lds_kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ aqs,
-                                                       const uint32_t* __restrict__ ads, float* __restrict__ Y,
-                                                       int K, int N, int64_t ldy_m, int64_t ldy_n,
-                                                       int items_per_wg, int32_t* __restrict__ dbg) {
+                                                       const uint32_t* __restrict__ ads,
+                                                       const float* __restrict__ X, int64_t sc, int64_t sk,
+                                                       float* __restrict__ Y, int K, int N, int64_t ldy_m,
+                                                       int64_t ldy_n, int items_per_wg, int32_t* __restrict__ dbg) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     GemvGeom g;
     g.K = K;
@@ -197,7 +220,10 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(const uint8_t* __restrict
 
     StepRegs A, B;
     if (total > 0) load_step<IR>(A, W, g, item, 0, slot, ib);  // first loads fly during the prologue
-    stage_activations(aqs, ads, C, K, sq, sdx, tid, blockDim.x);
+    if (kFuse)
+        quantize_to_lds(X, sc, sk, C, K, sq, sdx, tid, blockDim.x);
+    else
+        stage_activations(aqs, ads, C, K, sq, sdx, tid, blockDim.x);
     __syncthreads();
 
     float acc[IR][C];
@@ -272,8 +298,9 @@ static int device_cu_count() {
 }
 
 template <int C, int IR>
-static hipError_t launch_lds(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
-                             int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+static hipError_t launch_lds(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X, int64_t sc,
+                             int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
+                             hipStream_t stream) {
     const int64_t n_items = (N + IR - 1) / IR;
     const int64_t max_wgs = 2 * (int64_t)device_cu_count();
     int64_t wgs = (n_items + GEMV_WAVES_PER_WG - 1) / GEMV_WAVES_PER_WG;
@@ -283,27 +310,33 @@ static hipError_t launch_lds(const uint8_t* W, const int8_t* aqs, const uint32_t
     const size_t lds = (size_t)C * K + (size_t)C * (K / QK8_1) * 4 + (size_t)items_per_wg * IR * C * 4;
     if (lds > GEMV_LDS_BUDGET) return hipErrorNotSupported;
     const dim3 grid((unsigned)wgs), block(64 * GEMV_WAVES_PER_WG);
-    if (dbg)
-        hipLaunchKernelGGL((gemv_lds_kernel<C, IR, true>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N,
-                           ldy_m, ldy_n, (int)items_per_wg, dbg);
-    else
-        hipLaunchKernelGGL((gemv_lds_kernel<C, IR, false>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N,
-                           ldy_m, ldy_n, (int)items_per_wg, dbg);
+#define IQ4XS_LAUNCH_LDS(DBG, FUSE)                                                                              \
+    hipLaunchKernelGGL((gemv_lds_kernel<C, IR, DBG, FUSE>), grid, block, lds, stream, W, aqs, ads, X, sc, sk, Y,  \
+                       (int)K, (int)N, ldy_m, ldy_n, (int)items_per_wg, dbg)
+    if (X != nullptr) {
+        if (dbg) IQ4XS_LAUNCH_LDS(true, true); else IQ4XS_LAUNCH_LDS(false, true);
+    } else {
+        if (dbg) IQ4XS_LAUNCH_LDS(true, false); else IQ4XS_LAUNCH_LDS(false, false);
+    }
+#undef IQ4XS_LAUNCH_LDS
     return hipGetLastError();
 }
 
+// X == nullptr: planar Q8_1 activations (aqs, ads); otherwise fp32 X quantised
+// in the prologue (fused; returns hipErrorNotSupported when it does not fit).
 template <int C>
-static hipError_t launch_cols(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
-                              int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+static hipError_t launch_cols(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X, int64_t sc,
+                              int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
+                              hipStream_t stream) {
     const int64_t bpr = K / QK_K;
     hipError_t err = hipErrorNotSupported;
     if (K <= (1 << 24) && N < (1 << 30)) {
         if (bpr % 8 == 4)
-            err = launch_lds<C, 2>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
+            err = launch_lds<C, 2>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
         else
-            err = launch_lds<C, 1>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
+            err = launch_lds<C, 1>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
     }
-    if (err != hipErrorNotSupported) return err;
+    if (err != hipErrorNotSupported || X != nullptr) return err;
     const int64_t grid = (N + 3) / 4;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     if (dbg)
@@ -315,19 +348,30 @@ static hipError_t launch_cols(const uint8_t* W, const int8_t* aqs, const uint32_
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
-                       int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+static hipError_t dispatch_cols(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X, int64_t sc,
+                                int64_t sk, float* Y, int64_t K, int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n,
+                                int32_t* dbg, hipStream_t stream) {
     switch (M) {
-        case 1: return launch_cols<1>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
-        case 2: return launch_cols<2>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
-        case 3: return launch_cols<3>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
-        case 4: return launch_cols<4>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
-        case 5: return launch_cols<5>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
-        case 6: return launch_cols<6>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
-        case 7: return launch_cols<7>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
-        case 8: return launch_cols<8>(W, aqs, ads, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 1: return launch_cols<1>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 2: return launch_cols<2>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 3: return launch_cols<3>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 4: return launch_cols<4>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 5: return launch_cols<5>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 6: return launch_cols<6>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 7: return launch_cols<7>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 8: return launch_cols<8>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
+                       int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    return dispatch_cols(W, aqs, ads, nullptr, 0, 0, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
+}
+
+hipError_t launch_gemv_fused(const uint8_t* W, const float* X, int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N,
+                             int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    return dispatch_cols(W, nullptr, nullptr, X, sc, sk, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
 }
 
 }  // namespace iq4xs

@@ -24,6 +24,12 @@ hipError_t launch_planar_to_blocks(const int8_t* qs, const uint32_t* ds, int64_t
 hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
 
+// Same contract with fp32 activations quantised inside the kernel (element
+// (m, k) at X[m*sc + k*sk]); hipErrorNotSupported if the shape does not fit
+// the fused kernel's LDS budget (then quantise separately).
+hipError_t launch_gemv_fused(const uint8_t* W, const float* X, int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N,
+                             int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
+
 // Same contract on the int8 MFMA path (any M >= 1).
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);

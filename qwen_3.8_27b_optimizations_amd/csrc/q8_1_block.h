@@ -1,0 +1,64 @@
+// q8_1_block.h -- device-side Q8_1 quantisation of one 32-element block by
+// eight cooperating lanes, shared by the standalone quantiser and the fused
+// GEMV prologue.
+//
+// Semantics (real_stock_dp4a_comparator.hip:230-264): amax = max|x|,
+// sum = pairwise tree x[t]+x[t+16], +8, +4, +2, +1; d = amax/127 (IEEE);
+// q = amax ? (int8)roundf(x/d) : 0; ds = {rtz-fp16(d), rtz-fp16(sum)}.
+//
+// Lane j (0..7) of a group holds x[j], x[j+8], x[j+16], x[j+24]: the +16 and
+// +8 levels of the tree are in-lane, the +4/+2/+1 levels are ds_swizzle xor
+// steps inside the group.  Callers keep whole 8-lane groups active together.
+#pragma once
+
+#include "iq4xs_device.h"
+
+namespace iq4xs {
+
+template <int X>
+__device__ inline float swizzle_xor(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (X << 10)));
+}
+
+// roundf(x / d) with IEEE semantics, for |x| <= 127 * d.  p = x * rcp(d) lies
+// within 2^-15 of x/d (|x/d| <= 128, v_rcp_f32 error <= 1 ulp), and
+// RN(x/d) within 2^-17 of x/d, so both round to the same integer unless x/d
+// is within 2^-14 of a half-integer.  Those lanes -- and any non-finite p,
+// where the comparison is false -- take the exact division.
+static __device__ __attribute__((noinline)) int round_div_exact(float x, float d) { return (int)roundf(x / d); }
+
+__device__ inline int round_div(float x, float d, float r) {
+    const float p = x * r;
+    const float ap = fabsf(p);
+    const float f = ap - floorf(ap);
+    if (!(fabsf(f - 0.5f) >= 0x1p-14f)) return round_div_exact(x, d);
+    return (int)(p + copysignf(0.5f, p));
+}
+
+struct Q8Block8 {
+    int q0, q1, q2, q3;  // codes of x[j], x[j+8], x[j+16], x[j+24]
+    uint32_t ds;         // rtz-fp16(d) | rtz-fp16(sum) << 16 (identical in all 8 lanes)
+};
+
+__device__ inline Q8Block8 quantize_block8(float x0, float x1, float x2, float x3) {
+    float a = fmaxf(fmaxf(fabsf(x0), fabsf(x2)), fmaxf(fabsf(x1), fabsf(x3)));
+    float s = (x0 + x2) + (x1 + x3);
+    a = fmaxf(a, swizzle_xor<4>(a));
+    s = s + swizzle_xor<4>(s);
+    a = fmaxf(a, swizzle_xor<2>(a));
+    s = s + swizzle_xor<2>(s);
+    a = fmaxf(a, swizzle_xor<1>(a));
+    s = s + swizzle_xor<1>(s);
+    const float d = a / 127.0f;
+    Q8Block8 out{0, 0, 0, 0, float_to_half_bits_rtz(d) | (float_to_half_bits_rtz(s) << 16)};
+    if (a != 0.0f) {
+        const float r = __builtin_amdgcn_rcpf(d);
+        out.q0 = round_div(x0, d, r);
+        out.q1 = round_div(x1, d, r);
+        out.q2 = round_div(x2, d, r);
+        out.q3 = round_div(x3, d, r);
+    }
+    return out;
+}
+
+}  // namespace iq4xs

@@ -15,6 +15,7 @@
 //     consecutive floats; the tree is evaluated in registers.
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
+#include "q8_1_block.h"
 
 namespace iq4xs {
 
@@ -107,59 +108,34 @@ __global__ __launch_bounds__(256) void planar_to_blocks_kernel(const int8_t* __r
     for (int j = 0; j < 8; ++j) o[1 + j] = src[j];
 }
 
-// Row-contiguous layout (ggml src1, bs=1 vectors): eight lanes per block,
-// lane j holds x[j], x[j+8], x[j+16], x[j+24].  The reference tree is kept
-// exactly: x[t]+x[t+16] and the +8 level inside the lane, then xor-swizzles
-// 4, 2, 1 across the eight lanes (ds_swizzle in bitmask mode never crosses a
-// 32-lane half, and whole 8-lane groups are always active together).
-template <int X>
-__device__ inline float swizzle_xor(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (X << 10)));
-}
-
+// Row-contiguous layout (ggml src1, bs=1 vectors): eight lanes per block
+// (quantize_block8); whole 8-lane groups are always active together.
 __global__ __launch_bounds__(256) void quantize_q8_1_rows_kernel(const float* __restrict__ X, int64_t K, int64_t M,
                                                                  int8_t* __restrict__ qs, uint32_t* __restrict__ ds,
                                                                  block_q8_1* __restrict__ blocks) {
     const int64_t nb = K / QK8_1;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = t >> 3;
-    if (blk >= nb * M) return;  // whole 8-lane groups
+    if (blk >= nb * M) return;
     const int j = (int)(t & 7);
     const int64_t m = blk / nb, ib = blk - m * nb;
     const float* p = X + m * K + ib * QK8_1 + j;
-    const float x0 = p[0], x1 = p[8], x2 = p[16], x3 = p[24];
-    float a = fmaxf(fmaxf(fabsf(x0), fabsf(x2)), fmaxf(fabsf(x1), fabsf(x3)));
-    float s = (x0 + x2) + (x1 + x3);
-    a = fmaxf(a, swizzle_xor<4>(a));
-    s = s + swizzle_xor<4>(s);
-    a = fmaxf(a, swizzle_xor<2>(a));
-    s = s + swizzle_xor<2>(s);
-    a = fmaxf(a, swizzle_xor<1>(a));
-    s = s + swizzle_xor<1>(s);
-    const float d = a / 127.0f;
-    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-    if (a != 0.0f) {
-        q0 = (int)roundf(x0 / d);
-        q1 = (int)roundf(x1 / d);
-        q2 = (int)roundf(x2 / d);
-        q3 = (int)roundf(x3 / d);
-    }
-    const uint32_t dsw = float_to_half_bits_rtz(d) | (float_to_half_bits_rtz(s) << 16);
+    const Q8Block8 b = quantize_block8(p[0], p[8], p[16], p[24]);
     if (qs != nullptr) {
         int8_t* o = qs + m * K + ib * QK8_1 + j;
-        o[0] = (int8_t)q0;
-        o[8] = (int8_t)q1;
-        o[16] = (int8_t)q2;
-        o[24] = (int8_t)q3;
-        if (j == 0) ds[blk] = dsw;
+        o[0] = (int8_t)b.q0;
+        o[8] = (int8_t)b.q1;
+        o[16] = (int8_t)b.q2;
+        o[24] = (int8_t)b.q3;
+        if (j == 0) ds[blk] = b.ds;
     }
     if (blocks != nullptr) {
         int8_t* o = blocks[blk].qs + j;
-        o[0] = (int8_t)q0;
-        o[8] = (int8_t)q1;
-        o[16] = (int8_t)q2;
-        o[24] = (int8_t)q3;
-        if (j == 0) blocks[blk].ds = dsw;
+        o[0] = (int8_t)b.q0;
+        o[8] = (int8_t)b.q1;
+        o[16] = (int8_t)b.q2;
+        o[24] = (int8_t)b.q3;
+        if (j == 0) blocks[blk].ds = b.ds;
     }
 }
 

@@ -123,6 +123,43 @@ def test_q8_1_special_blocks(pkg, orc, dev):
     assert np.array_equal(got, orc.quantize_q8_1(x))
 
 
+def rounding_boundary_blocks(n_blocks: int, seed: int) -> np.ndarray:
+    """Blocks whose x/d sit on or within a few ulp-scale offsets of half
+    integers (the quantiser's reciprocal fast path must hand those to the
+    exact division), plus blocks of fp32 denormals and mixed magnitudes."""
+    rng = np.random.default_rng(seed)
+    out = np.zeros((n_blocks, 32), np.float32)
+    offs = np.array([0.0, 2.0**-22, -2.0**-22, 2.0**-16, -2.0**-16, 2.0**-14, -2.0**-14,
+                     2.0**-13, -2.0**-13, 2.0**-10, -2.0**-10])
+    for b in range(n_blocks):
+        kind = b % 4
+        if kind == 3:  # denormal block (d stays > 0)
+            out[b] = (rng.standard_normal(32) * 1e-39).astype(np.float32)
+            continue
+        amax = np.float32(10.0 ** rng.uniform(-6, 4))
+        d = np.float32(amax / np.float32(127.0))
+        k = rng.integers(-127, 127, 32)
+        x = (k + 0.5 + rng.choice(offs, 32)) * np.float64(d)
+        if kind == 1:
+            x *= rng.choice([1.0, 1e-3], 32)  # mixed magnitudes inside one block
+        out[b] = x.astype(np.float32)
+        out[b, rng.integers(32)] = amax * rng.choice([-1.0, 1.0])
+    return out.ravel()
+
+
+def test_q8_1_rounding_boundaries(pkg, orc, dev):
+    K = 256 * 64
+    x = rounding_boundary_blocks(K // 32, seed=11)
+    ref = orc.quantize_q8_1(x)
+    ws = pkg.quantize_q8_1(D(x, dev), K, 1, LAYOUT_MK)
+    got = pkg.q8_1_blocks(ws, K, 1).cpu().numpy().ravel()
+    assert np.array_equal(got, ref)
+    X = x.reshape(8, K // 8)
+    ws = pkg.quantize_q8_1(D(np.ascontiguousarray(X.T), dev), K // 8, 8, LAYOUT_KM)
+    got = pkg.q8_1_blocks(ws, K // 8, 8).cpu().numpy().ravel()
+    assert np.array_equal(got, orc.quantize_q8_1_batched(X, K // 8, 8, LAYOUT_MK))
+
+
 # ------------------------------------------------------------------ GEMV / GEMM kernels
 GEMV_CASES = [(256, 1, 1), (768, 7, 1), (1024, 64, 1), (5120, 333, 1), (4096, 4096, 1),
               (768, 9, 2), (1280, 65, 3), (2048, 130, 4), (256, 5, 5), (5120, 100, 6), (512, 77, 7),
@@ -142,6 +179,44 @@ def test_gemv_sums_and_outputs(pkg, orc, dev, K, N, M):
     assert np.array_equal(S.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, M))
     check_outputs(orc, W, AQ, Y.cpu().numpy(), K, N, M, "gemv+dbg")
     assert torch.equal(Y, Y2)  # the debug store does not change the arithmetic
+
+
+FUSED_CASES = [(256, 1, 1, LAYOUT_MK), (5120, 333, 1, LAYOUT_MK), (17408, 40, 1, LAYOUT_MK),
+               (768, 9, 2, LAYOUT_KM), (2048, 130, 4, LAYOUT_MK), (5120, 100, 6, LAYOUT_KM),
+               (8192, 96, 7, LAYOUT_MK), (5120, 64, 8, LAYOUT_KM)]
+
+
+@pytest.mark.parametrize("K,N,M,layout", FUSED_CASES)
+def test_fused_quantize_gemv(pkg, orc, dev, K, N, M, layout):
+    """One-launch path (Q8_1 quantisation in the GEMV prologue) == the
+    two-launch path bit for bit: same codes, same d, same summation order."""
+    W = orc.gen_weights(K, N, seed=5000 + K + N)
+    X = orc.gen_activations(K * M, seed=6000 + M, outliers=True).reshape(M, K)
+    if M == 1 and K == 5120:
+        X = rounding_boundary_blocks(K // 32, seed=12).reshape(1, K)
+    AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
+    Wd = D(W, dev)
+    Xd = D(X if layout == LAYOUT_MK else X.T, dev)
+    Yf, Sf = pkg.mul_mat_fused(Wd, Xd, K, N, M, layout, sums=True)
+    ws = pkg.quantize_q8_1(Xd, K, M, layout)
+    Yp = pkg.mul_mat_q8_1(Wd, ws, K, N, M, layout, pkg.PATH_GEMV)
+    torch.cuda.synchronize()
+    assert np.array_equal(Sf.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, M))
+    assert torch.equal(Yf, Yp)
+    Ymn = Yf.cpu().numpy() if layout == LAYOUT_MK else Yf.cpu().numpy().T
+    check_outputs(orc, W, AQ, Ymn, K, N, M, "fused")
+
+
+def test_fused_rejects_oversized_activations(pkg, dev):
+    K, N, M = 17408, 64, 8  # 8 x 17408 codes exceed the on-chip activation buffer
+    W = torch.zeros(N * K // 256 * 136, dtype=torch.uint8, device=dev)
+    X = torch.zeros((M, K), dtype=torch.float32, device=dev)
+    with pytest.raises(pkg.Iq4xsError) as e:
+        pkg.mul_mat_fused(W, X, K, N, M)
+    assert e.value.code == pkg.ERROR_NOT_SUPPORTED
+    with pytest.raises(pkg.Iq4xsError) as e:
+        pkg.mul_mat_fused(W, X, K, N, 9)
+    assert e.value.code == pkg.ERROR_NOT_SUPPORTED
 
 
 GEMM_CASES = [(256, 64, 64), (256, 1, 1), (512, 100, 20), (768, 130, 65), (1024, 64, 128),
