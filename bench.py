@@ -3,19 +3,25 @@
 Workload (the headline metric's configuration): the 27B-class decode linear
 set at batch 1 -- q_proj 5120->8192, k_proj/v_proj 5120->1024, o_proj
 8192->5120, gate_proj/up_proj 5120->17408, down_proj 17408->5120 -- each run
-as its own quantise + GEMV through the C ABI.  One step = the seven
-projections of one layer.  `--layers` distinct layer copies (default 16 =
-3.07 GB of IQ4_XS) are generated on the device and rotated, so the 256 MB
-Infinity Cache cannot serve repeats: every step streams its weights from HBM.
-Steps are captured once into a HIP graph and replayed.
+as its own call of the C ABI (fp32 activations in, fp32 outputs out: the Q8_1
+quantisation is part of the call).  One step = the seven projections of one
+layer.  `--layers` distinct layer copies (default 16 = 3.07 GB of IQ4_XS) are
+generated on the device and rotated, so the 256 MB Infinity Cache cannot
+serve repeats: every step streams its weights from HBM.  A rotation of steps
+is captured once into a HIP graph and replayed.
 
-value = algorithmic bytes per step (sum of N*K*136/256 + 4K + 4N over the
-seven GEMVs) / time per step.  roofline = the GEMV kernel alone: the same
-bytes over its average launch duration from HIP event pairs around each
-launch.  gemm = the int8-MFMA GEMM at M=512 on the same shapes, 2*M*N*K over
-kernel time.  cpu_baseline = the reference's own FP64 oracle
-(kernels/matmul_iq4xs/ref_cpu.cpp, compiled into oracle/_ref) -- or this
-repository's restatement where that is absent -- on one host core.
+value     algorithmic bytes per step (sum of N*K*136/256 + 4K + 4N over the
+          seven GEMVs) / time per step.
+roofline  the GEMV kernel alone, on prequantised Q8_1 activations: a graph of
+          the seven GEMV launches of every layer copy (no quantiser), timed
+          with HIP events on the launch stream; achieved = the same
+          algorithmic bytes / average launch duration.
+extra     bs = 2, 4, 8 (the same GEMV-only measurement with 1 % x20
+          outliers) and the int8-MFMA GEMM at M = 512 and 2048 (2*M*N*K over
+          the average of back-to-back launches rotated over the layer copies).
+cpu_baseline  the reference's own FP64 oracle (kernels/matmul_iq4xs/ref_cpu.cpp,
+          compiled into oracle/_ref) -- or this repository's restatement where
+          that is absent -- on one host core, on a bounded sample.
 """
 from __future__ import annotations
 
@@ -47,7 +53,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--layers", type=int, default=16)
-    ap.add_argument("--gemm-m", type=int, default=512)
+    ap.add_argument("--roofline-reps", type=int, default=32, help="replays of the GEMV-only rotation graph")
+    ap.add_argument("--gemm-m", type=int, nargs="*", default=[512, 2048])
+    ap.add_argument("--batches", type=int, nargs="*", default=[2, 4, 8])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -57,8 +65,6 @@ def parse():
 def cpu_baseline(seconds: float) -> dict:
     """FP64 oracle GEMVs of one layer's seven projections on one host core,
     repeated until `seconds` elapse (bounded sample of the same workload)."""
-    import numpy as np
-
     from oracle.oracle import Oracle, RefCpu, ref_available
 
     orc = Oracle()
@@ -90,11 +96,48 @@ def cpu_baseline(seconds: float) -> dict:
             "ms_per_step": round(el / passes * 1e3, 2)}
 
 
+class Timer:
+    """Events recorded on the launch stream around a callable run `reps` times."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def __call__(self, fn, reps: int) -> float:
+        torch = self.torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(self.stream)
+        for _ in range(reps):
+            fn()
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3  # microseconds
+
+
+def capture(torch, stream, fn, use_graph: bool):
+    """A graph of fn (one warm run first), or fn itself when graphs are off or fail."""
+    fn()
+    torch.cuda.synchronize()
+    if not use_graph:
+        return fn, "eager"
+    try:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        return g.replay, "hipgraph"
+    except Exception as e:  # capture unsupported: fall back to eager launches
+        print(f"[bench] graph capture failed ({e}); timing eager launches", file=sys.stderr)
+        return fn, "eager"
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the IQ4_XS path has no multi-GPU mode in this build "
-              "(rows shard independently; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(rows shard independently across GPUs; the sharding design is documented with the "
+              "library). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
@@ -108,6 +151,8 @@ def main() -> int:
     stream = torch.cuda.Stream()  # default priority
     torch.cuda.set_stream(stream)
     s = stream.cuda_stream
+    timer = Timer(torch, stream)
+    use_graph = not args.no_graph
 
     # ---- resident inputs -------------------------------------------------
     layers = []
@@ -122,102 +167,84 @@ def main() -> int:
     ys = [torch.empty(N, device=dev) for (_, _, N) in SHAPES]
     wss = [torch.empty(L.iq4xs_workspace_bytes(K, 1), dtype=torch.uint8, device=dev) for (_, K, _) in SHAPES]
     torch.cuda.synchronize()
-
-    def one_step(l: int) -> None:
-        for i, (_, K, N) in enumerate(SHAPES):
-            L.check("iq4xs_mul_mat", layers[l][i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), K, N, 1,
-                    pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
-
     step_bytes = sum(gemv_bytes(K, N) for _, K, N in SHAPES)
+    n_launch = args.layers * len(SHAPES)
 
-    # ---- whole-step timing: graph of one rotation over all layers ----------
-    launch = "eager"
-    graph = None
-    if not args.no_graph:
-        try:
-            for l in range(args.layers):
-                one_step(l)  # warm every code path before capture
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                for l in range(args.layers):
-                    one_step(l)
-            launch = "hipgraph"
-        except Exception as e:  # capture unsupported: fall back to eager launches
-            print(f"[bench] graph capture failed ({e}); timing eager launches", file=sys.stderr)
-            graph = None
+    # ---- headline: whole steps (quantise + GEMV per projection) ------------
+    def rotation() -> None:
+        for l in range(args.layers):
+            for i, (_, K, N) in enumerate(SHAPES):
+                L.check("iq4xs_mul_mat", layers[l][i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), K, N, 1,
+                        pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
+
+    run, launch = capture(torch, stream, rotation, use_graph)
     reps = max(1, -(-args.steps // args.layers))
-    steps = reps * args.layers
     warm_reps = max(1, -(-args.warmup // args.layers))
-
-    def run_rotation() -> None:
-        if graph is not None:
-            graph.replay()
-        else:
-            for l in range(args.layers):
-                one_step(l)
-
-    for _ in range(warm_reps):
-        run_rotation()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(reps):
-        run_rotation()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_total = t0.elapsed_time(t1)
-    ms_per_step = ms_total / steps
+    timer(run, warm_reps)
+    us_total = timer(run, reps)
+    steps = reps * args.layers
+    ms_per_step = us_total / steps / 1e3
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # ---- GEMV kernel alone: event pair around every launch ----------------
-    ev_pairs = []
-    for l in range(args.layers):
-        for i, (_, K, N) in enumerate(SHAPES):
-            L.check("iq4xs_quantize_q8_1", xs[i].data_ptr(), K, 1, pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            L.check("iq4xs_mul_mat_q8_1", layers[l][i].data_ptr(), wss[i].data_ptr(), ys[i].data_ptr(), K, N, 1,
-                    pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
-            b.record(stream)
-            ev_pairs.append((i, a, b))
-    torch.cuda.synchronize()
-    per_shape_us = {name: [] for name, _, _ in SHAPES}
-    for i, a, b in ev_pairs:
-        per_shape_us[SHAPES[i][0]].append(a.elapsed_time(b) * 1e3)
-    gemv_us = sum(sum(v) for v in per_shape_us.values())
-    gemv_launches = len(ev_pairs)
+    # ---- roofline: the GEMV kernel alone on prequantised activations --------
+    def gemv_rotation(wsb, yb, M) -> None:
+        for l in range(args.layers):
+            for i, (_, K, N) in enumerate(SHAPES):
+                L.check("iq4xs_mul_mat_q8_1", layers[l][i].data_ptr(), wsb[i].data_ptr(), yb[i].data_ptr(), K, N,
+                        M, pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
+
+    for i, (_, K, _) in enumerate(SHAPES):
+        L.check("iq4xs_quantize_q8_1", xs[i].data_ptr(), K, 1, pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
+    grun, _ = capture(torch, stream, lambda: gemv_rotation(wss, ys, 1), use_graph)
+    timer(grun, 2)
+    gemv_us = timer(grun, args.roofline_reps) / args.roofline_reps
+    avg_launch_us = gemv_us / n_launch
     achieved = step_bytes * args.layers / (gemv_us * 1e-6) / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
-    # ---- GEMM at M = gemm_m on the same shapes -----------------------------
-    M = args.gemm_m
-    gemm_ops, gemm_us, gemm_shape_us = 0, 0.0, {}
-    for i, (name, K, N) in enumerate(SHAPES):
-        X = pkg.synthetic_activations(K * M, seed=300 + i, device=dev)
-        ws = pkg.quantize_q8_1(X, K, M)
-        Y = torch.empty((M, N), device=dev)
-        W = layers[0][i]
-        for _ in range(3):
-            pkg.mul_mat_q8_1(W, ws, K, N, M, out=Y)
-        times = []
-        for r in range(10):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            pkg.mul_mat_q8_1(layers[r % args.layers][i], ws, K, N, M, out=Y)
-            b.record(stream)
-            times.append((a, b))
-        torch.cuda.synchronize()
-        us = sorted(a.elapsed_time(b) * 1e3 for a, b in times)[len(times) // 2]
-        gemm_shape_us[name] = round(us, 2)
-        gemm_ops += 2 * M * N * K
-        gemm_us += us
-        del X, ws, Y
-    gemm_tops = gemm_ops / (gemm_us * 1e-6) / 1e12
+    # ---- small batch (bs = 2, 4, 8), GEMV kernel on prequantised columns ----
+    small = {}
+    for M in args.batches:
+        X = [pkg.synthetic_activations(K * M, seed=500 + M + i, outliers=True, device=dev)
+             for i, (_, K, _) in enumerate(SHAPES)]
+        wsb = [pkg.quantize_q8_1(X[i], K, M) for i, (_, K, _) in enumerate(SHAPES)]
+        yb = [torch.empty((M, N), device=dev) for (_, _, N) in SHAPES]
+        brun, _ = capture(torch, stream, lambda: gemv_rotation(wsb, yb, M), use_graph)
+        timer(brun, 2)
+        us = timer(brun, max(4, args.roofline_reps // 4)) / max(4, args.roofline_reps // 4)
+        b_bytes = sum(gemv_bytes(K, N, M) for _, K, N in SHAPES) * args.layers
+        small[str(M)] = {"GBps": round(b_bytes / (us * 1e-6) / 1e9, 1),
+                         "frac": round(b_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "us_per_layer": round(us / args.layers, 2)}
+        del X, wsb, yb, brun
+
+    # ---- GEMM at M = 512 / 2048 on the same shapes -------------------------
+    gemm = {}
+    for M in args.gemm_m:
+        ops, us_sum, per_shape = 0, 0.0, {}
+        for i, (name, K, N) in enumerate(SHAPES):
+            X = pkg.synthetic_activations(K * M, seed=300 + i, device=dev)
+            ws = pkg.quantize_q8_1(X, K, M)
+            Y = torch.empty((M, N), device=dev)
+            nrep = 8 if M >= 2048 else 16
+            for _ in range(2):
+                pkg.mul_mat_q8_1(layers[0][i], ws, K, N, M, out=Y)
+            ctr = [0]
+
+            def one():
+                pkg.mul_mat_q8_1(layers[ctr[0] % args.layers][i], ws, K, N, M, out=Y)
+                ctr[0] += 1
+
+            us = timer(one, nrep) / nrep
+            per_shape[name] = round(us, 2)
+            ops += 2 * M * N * K
+            us_sum += us
+            del X, ws, Y
+        tops = ops / (us_sum * 1e-6) / 1e12
+        gemm[str(M)] = {"tops": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4), "per_shape_us": per_shape}
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
@@ -236,18 +263,16 @@ def main() -> int:
         "data": "synthetic (seeded IQ4_XS weights d~U(0.005,0.02), ls~U{0..63}, codes~U{0..15}; x~N(0,1)), "
                 "generated on the device",
         "config": {"workload": "qwen27b-class decode linear set, bs=1: 7 projection GEMVs per step "
-                               "(quantise + GEMV each), weights HBM-resident",
+                               "(fp32 activations quantised to Q8_1 inside each call), weights HBM-resident",
                    "shapes_KxN": {n: [K, N] for n, K, N in SHAPES}, "batch": 1,
                    "layers_rotated": args.layers, "weight_bytes_resident": step_bytes * args.layers,
                    "launch": launch, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_iq4xs_kernel<1,2,false>",
-                     "avg_launch_us": round(gemv_us / gemv_launches, 3),
-                     "per_shape_avg_us": {k: round(sum(v) / len(v), 3) for k, v in per_shape_us.items()}},
-        "gemm": {"M": M, "tops": round(gemm_tops, 2), "peak_tops": INT8_PEAK_TOPS,
-                 "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "per_shape_us": gemm_shape_us,
-                 "kernel": "gemm_iq4xs_mfma_kernel<false>"},
+                     "kernel": "gemv_tile_kernel<1,2,false,false> (bs=1, prequantised Q8_1)",
+                     "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps},
+        "small_batch_gemv": small,
+        "gemm": {"peak_tops": INT8_PEAK_TOPS, "kernel": "gemm_iq4xs_mfma_kernel", "by_M": gemm},
         "cpu_baseline": cpu,
         "host": platform.node(),
     }

@@ -68,10 +68,31 @@ hipError_t mul_mat_planar(const uint8_t* W, const void* ws, float* Y, int64_t K,
     return hipErrorInvalidValue;
 }
 
+// Single-column calls with K up to this bound run the GEMV with the Q8_1
+// quantisation in its prologue (one launch, no workspace).  Every workgroup
+// quantises the whole column, so the prologue grows with K: past this bound
+// (and for M > 1) a separate quantiser launch is cheaper.
+constexpr int64_t FUSED_MAX_K = 6144;
+
+bool prefer_fused(int64_t K, int64_t M) { return M == 1 && K <= FUSED_MAX_K; }
+
+hipError_t mul_mat_fused(const uint8_t* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                         int32_t* dbg, hipStream_t stream) {
+    const int64_t ldy_m = (layout == LAYOUT_MK) ? N : 1;
+    const int64_t ldy_n = (layout == LAYOUT_MK) ? 1 : M;
+    const int64_t sc = (layout == LAYOUT_MK) ? K : 1;
+    const int64_t sk = (layout == LAYOUT_MK) ? 1 : M;
+    return launch_gemv_fused(W, X, sc, sk, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
+}
+
 // quantise + multiply with scratch from the stream-ordered pool
 hipError_t mul_mat_pooled(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
                           hipStream_t stream) {
     if (!valid_mat(W, X, Y, K, N, M)) return hipErrorInvalidValue;
+    if (prefer_fused(K, M)) {
+        const hipError_t e = mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, nullptr, stream);
+        if (e != hipErrorNotSupported) return e;
+    }
     void* ws = nullptr;
     hipError_t err = pool_alloc(&ws, planar_bytes(K, M), stream);
     if (err != hipSuccess) return err;
@@ -154,6 +175,13 @@ int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64
 int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
                   size_t ws_bytes, void* stream) {
     if (!valid_mat(W, X, Y, K, N, M) || !ws) return hipErrorInvalidValue;
+    if ((layout != LAYOUT_KM && layout != LAYOUT_MK) || ws_bytes < planar_bytes(K, M)) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
+    if (prefer_fused(K, M)) {
+        const hipError_t e =
+            mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, nullptr, as_stream(stream));
+        if (e != hipErrorNotSupported) return e;
+    }
     const int err = iq4xs_quantize_q8_1(X, K, M, layout, ws, ws_bytes, stream);
     if (err != hipSuccess) return err;
     return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, IQ4XS_PATH_AUTO, nullptr,
@@ -164,12 +192,7 @@ int iq4xs_mul_mat_fused(const void* W, const float* X, float* Y, int64_t K, int6
                         int32_t* S, void* stream) {
     if (!valid_mat(W, X, Y, K, N, M) || (layout != LAYOUT_KM && layout != LAYOUT_MK)) return hipErrorInvalidValue;
     if (M > GEMV_MAX_COLS) return hipErrorNotSupported;
-    const int64_t ldy_m = (layout == LAYOUT_MK) ? N : 1;
-    const int64_t ldy_n = (layout == LAYOUT_MK) ? 1 : M;
-    const int64_t sc = (layout == LAYOUT_MK) ? K : 1;
-    const int64_t sk = (layout == LAYOUT_MK) ? 1 : M;
-    return launch_gemv_fused(static_cast<const uint8_t*>(W), X, sc, sk, Y, K, N, M, ldy_m, ldy_n, S,
-                             as_stream(stream));
+    return mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, S, as_stream(stream));
 }
 
 int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, void* stream) {

@@ -7,26 +7,27 @@
 // The int32 sumi of every sub-block is exact (bit-identical to the
 // reference); only the fp32 summation order differs.
 //
-// MI355X mapping (streaming kernel, gemv_lds_kernel).  On this path the
-// VALU work per weight byte decides how well HBM streaming overlaps with
-// compute, so the kernel is built to spend as few instructions per 16 bytes
-// of weights as possible:
-//   * lane l handles sub-block (l & 7) of super-block (l >> 3) of an
-//     8-super-block "step": one dwordx4 per lane reads 1088 contiguous bytes
-//     of a row per wave, straight from HBM;
-//   * a work item is one row, or two adjacent rows when K/256 = 4 mod 8
-//     (K = 5120, 17408): the two rows' super-blocks are contiguous, so a
-//     2-row item is exactly (2K/256)/8 full steps and no lane idles;
-//   * the Q8_1 activations (codes + fp32 d) sit in LDS, copied or quantised
-//     once per workgroup; workgroups are persistent (about two per CU) and
-//     walk a contiguous range of items;
-//   * each wave keeps the next step's loads in flight while it computes the
-//     current one; row sums are reduced with DPP, parked in LDS and written
-//     once at the end, so no store sits inside the streaming loop;
-//   * codebook decode: decode_codes_x (perm "specials", 11 ops / 8 codes).
-// gemv_global_kernel is the fallback for shapes whose activations do not fit
-// the LDS budget (large K with many columns): same arithmetic, activations
-// read through L1/L2.
+// MI355X mapping.  The unit of work is a "step": 8 consecutive 136-byte
+// super-blocks (1088 B).  Lane l of a wave handles sub-block (l & 7) of
+// super-block (l >> 3): one 16-byte load of codes plus the 8-byte block header
+// per lane.  The codebook decode is decode_codes_x (v_perm "specials", 11 ops
+// per 8 codes), the integer dot is v_dot4_i32_i8, and activations (codes + d)
+// are read from LDS.
+//   gemv_tile_kernel   (default, K >= 2048): short-lived workgroups that own a
+//       few whole rows; waves interleave the tile's steps, so the grid sweeps
+//       the matrix in address order; a ring of D register buffers keeps D-1
+//       steps in flight during compute; super-block partials meet in LDS and
+//       rows are summed in a fixed order.
+//   gemv_flat_kernel   (when the tile's LDS would not fit, e.g. 8 columns at
+//       K = 5120): each wave streams one contiguous range of steps and reduces
+//       a row whenever it ends (DPP), row pieces meet in LDS.
+//   gemv_lds_kernel    (K < 2048): one or two rows per work item.
+//   gemv_global_kernel (activations too large for LDS): activations read
+//       through L1/L2.
+// Environment overrides for tuning (IQ4XS_GEMV_*) are read once per process.
+#include <numeric>
+#include <stdlib.h>
+
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 #include "q8_1_block.h"
@@ -167,22 +168,44 @@ __device__ inline void stage_activations(const int8_t* __restrict__ aqs, const u
 
 // Fused prologue: quantise the fp32 activations (element (c, k) at
 // X[c*sc + k*sk]) straight into LDS, eight lanes per block.  Only d is kept:
-// the dot uses the fp16-truncated d exactly as the planar path does.
+// the dot uses the fp16-truncated d exactly as the planar path does.  Loads of
+// up to four rounds are issued before any of them is used, so the prologue
+// costs about one memory latency rather than one per round.
 __device__ inline void quantize_to_lds(const float* __restrict__ X, int64_t sc, int64_t sk, int C, int K, int8_t* sq,
                                        float* sdx, int tid, int nthreads) {
+    constexpr int U = 4;
     const int nb = K / QK8_1;
-    const int tasks = C * nb * 8;  // nthreads is a multiple of 64: 8-lane groups stay whole
-    for (int t = tid; t < tasks; t += nthreads) {
-        const int blk = t >> 3, j = t & 7;
-        const int cc = blk / nb, ib = blk - cc * nb;
-        const float* p = X + cc * sc + (int64_t)(ib * QK8_1 + j) * sk;
-        const Q8Block8 b = quantize_block8(p[0], p[8 * sk], p[16 * sk], p[24 * sk]);
-        int8_t* o = sq + cc * K + ib * QK8_1 + j;
-        o[0] = (int8_t)b.q0;
-        o[8] = (int8_t)b.q1;
-        o[16] = (int8_t)b.q2;
-        o[24] = (int8_t)b.q3;
-        if (j == 0) sdx[blk] = half_bits_to_float(b.ds & 0xFFFFu);
+    const int tasks = C * nb * 8;  // a multiple of 64 (K % 256 == 0): 8-lane groups and waves stay whole
+    for (int t0 = tid; t0 < tasks; t0 += U * nthreads) {
+        float x[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + u * nthreads;
+            if (t < tasks) {
+                const int blk = t >> 3, j = t & 7;
+                const int cc = blk / nb, ib = blk - cc * nb;
+                const float* p = X + cc * sc + (int64_t)(ib * QK8_1 + j) * sk;
+                x[u][0] = p[0];
+                x[u][1] = p[8 * sk];
+                x[u][2] = p[16 * sk];
+                x[u][3] = p[24 * sk];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + u * nthreads;
+            if (t < tasks) {
+                const int blk = t >> 3, j = t & 7;
+                const int cc = blk / nb, ib = blk - cc * nb;
+                const Q8Block8 b = quantize_block8(x[u][0], x[u][1], x[u][2], x[u][3]);
+                int8_t* o = sq + cc * K + ib * QK8_1 + j;
+                o[0] = (int8_t)b.q0;
+                o[8] = (int8_t)b.q1;
+                o[16] = (int8_t)b.q2;
+                o[24] = (int8_t)b.q3;
+                if (j == 0) sdx[blk] = half_bits_to_float(b.ds & 0xFFFFu);
+            }
+        }
     }
 }
 
@@ -281,6 +304,298 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(const uint8_t* __restrict
     }
 }
 
+// ---------------------------------------------------------------- flat-stream kernel
+// The weight matrix is one contiguous array of N*bpr super-blocks.  A
+// workgroup owns rows [r0, r0 + rows_per_wg) (r0*bpr a multiple of 8, so its
+// range starts on a step boundary); its steps of 8 super-blocks are split into
+// equal contiguous ranges, one per wave, whatever the row length.  A wave
+// streams its range through a ring of D register buffers (each reloaded right
+// after it is consumed, so D-1 steps stay in flight during compute), keeps one
+// fp32 accumulator per lane and column, and reduces it whenever its current
+// row ends (a row may end inside a step: lanes past the end start the next
+// row).  Row pieces of neighbouring waves meet in LDS and are summed there in
+// wave order, so the result does not depend on timing.
+constexpr int FLAT_WAVES = 8;
+
+template <int C>
+__device__ inline void flat_flush(float (&acc)[C], float* part, int wave, int J, int j, int lane) {
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) {
+        const float v = wave_sum_dpp(acc[cc]);
+        if (lane == 0) part[(wave * J + j) * C + cc] = v;
+    }
+}
+
+template <int C, int D, bool kDebug, bool kFuse>
+__global__ __launch_bounds__(64 * FLAT_WAVES) void gemv_flat_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ aqs, const uint32_t* __restrict__ ads,
+    const float* __restrict__ X, int64_t sc, int64_t sk, float* __restrict__ Y, int K, int N, int64_t ldy_m,
+    int64_t ldy_n, int rows_per_wg, int J, int32_t* __restrict__ dbg) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bpr = K / QK_K, nb = K / QK8_1;
+    int8_t* sq = reinterpret_cast<int8_t*>(lds);
+    float* sdx = reinterpret_cast<float*>(lds + (size_t)C * K);
+    float* part = sdx + C * nb;                 // [FLAT_WAVES][J][C]
+    int* wrows = reinterpret_cast<int*>(part + FLAT_WAVES * J * C);  // [FLAT_WAVES][2]: first row, count
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, slot = lane >> 3, ib = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nrows = min(rows_per_wg, N - r0);
+    const int n_sb = nrows * bpr;
+    const int n_steps = (n_sb + 7) >> 3;
+    const int q = n_steps / FLAT_WAVES, rem = n_steps - q * FLAT_WAVES;
+    const int s_a = wave * q + min(wave, rem);
+    const int s_b = s_a + q + (wave < rem ? 1 : 0);
+    const uint8_t* Wg = W + (size_t)r0 * bpr * BLOCK_BYTES;
+
+    // Loads of step s (clamped into the workgroup's range; clamped lanes are
+    // never accumulated).
+    // Step s (0 <= s < n_steps) starts at the wave-uniform address
+    // Wg + s*1088; each lane adds its constant offset.  Only the workgroup's
+    // last step can be ragged: there lanes past the end re-read the last
+    // super-block and are not accumulated.
+    const int last_step = n_steps - 1;
+    const int last_slot = (n_sb - 1) - 8 * last_step;
+    const uint32_t off_n = (uint32_t)slot * BLOCK_BYTES;
+    const uint32_t off_l = (uint32_t)min(slot, last_slot) * BLOCK_BYTES;
+    const uint32_t off_q = 16u * (uint32_t)ib;
+    auto load = [&](StepRegs& r, int s) {
+        const uint8_t* base = Wg + (size_t)s * (8 * BLOCK_BYTES);  // scalar
+        const uint32_t o = s == last_step ? off_l : off_n;         // lane offset
+        r.h = *reinterpret_cast<const v2u*>(base + o);
+        r.q = *reinterpret_cast<const v4i_a8*>(base + (o + off_q) + 8);
+    };
+
+    // The first D-1 steps of weights fly while the activations are staged
+    // (both latencies overlap; vmcnt retires in order, so the staging waits
+    // for these loads as well -- keep D small).
+    StepRegs buf[D];
+    if (s_a < s_b) {
+#pragma unroll
+        for (int d = 0; d < D - 1; ++d) load(buf[d], min(s_a + d, s_b - 1));
+    }
+    if (kFuse)
+        quantize_to_lds(X, sc, sk, C, K, sq, sdx, tid, blockDim.x);
+    else
+        stage_activations(aqs, ads, C, K, sq, sdx, tid, blockDim.x);
+    __syncthreads();
+
+    float acc[C];
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) acc[cc] = 0.0f;
+    const int R_first = (8 * s_a) / bpr;
+    int R = R_first;                 // current row, relative to r0 (wave-uniform)
+    int row_end = (R + 1) * bpr;     // first super-block past row R
+    const int sh_lo = 4 * ib, sh_hi = 16 + 2 * ib;
+
+    auto compute = [&](const StepRegs& cur, int s) {
+        const int sb = 8 * s + slot;
+        const bool valid = s != last_step || slot <= last_slot;
+        const bool nxt = sb >= row_end;     // lane already in row R+1
+        // sub-block index inside the lane's row
+        const int a_idx = 8 * (8 * s - (row_end - bpr)) + lane - (nxt ? nb : 0);
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)cur.q[j], lo[j], hi[j]);
+        const int ls = (int)(((cur.h.y >> sh_lo) & 0xFu) | (((cur.h.x >> sh_hi) & 0x3u) << 4)) - 32;
+        const float dw = half_bits_to_float(cur.h.x & 0xFFFFu);
+        float t[C];
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc) {
+            const v4i* pa = reinterpret_cast<const v4i*>(sq + cc * K + a_idx * QK8_1);
+            const v4i a0 = pa[0], a1 = pa[1];
+            int sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sum = dot4(lo[j], (uint32_t)a0[j], sum);
+                sum = dot4(hi[j], (uint32_t)a1[j], sum);
+            }
+            sum = __mul24(sum, ls);
+            t[cc] = valid ? (dw * sdx[cc * nb + a_idx]) * (float)sum : 0.0f;
+            if (kDebug && valid) dbg[((int64_t)cc * N + r0 + R + (nxt ? 1 : 0)) * nb + a_idx] = sum;
+        }
+        if (8 * s + 8 < row_end) {
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc) acc[cc] += t[cc];
+        } else {                            // row R ends in this step
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc) acc[cc] += nxt ? 0.0f : t[cc];
+            flat_flush<C>(acc, part, wave, J, R - R_first, lane);
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc) acc[cc] = nxt ? t[cc] : 0.0f;
+            ++R;
+            row_end += bpr;
+        }
+    };
+    // Sub-step d first refills the buffer consumed by sub-step d-1 (step
+    // s+d+D-1), then computes step s+d: D-1 steps are in flight during every
+    // compute.  Loads are unconditional (clamped), so the wait counts stay
+    // exact across the back edge; only the compute of steps past the end is
+    // skipped.  One copy of the body per ring slot keeps the code small: with
+    // a handful of steps per wave, instruction fetch is on the critical path.
+    for (int s = s_a; s < s_b; s += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            load(buf[(d + D - 1) % D], min(s + d + D - 1, s_b - 1));
+            if (s + d < s_b) compute(buf[d], s + d);
+        }
+    }
+    int count = R - R_first;
+    if (s_a < s_b && R * bpr < min(8 * s_b, n_sb)) {  // unfinished row piece
+        flat_flush<C>(acc, part, wave, J, R - R_first, lane);
+        ++count;
+    }
+    if (lane == 0) {
+        wrows[2 * wave] = R_first;
+        wrows[2 * wave + 1] = s_a < s_b ? count : 0;
+    }
+    __syncthreads();
+    // Branch-free combine: every wave's piece of row rl (clamped index, masked
+    // value), summed in wave order.  All LDS reads issue back to back.
+    int f[FLAT_WAVES], n[FLAT_WAVES];
+#pragma unroll
+    for (int w = 0; w < FLAT_WAVES; ++w) {
+        f[w] = wrows[2 * w];
+        n[w] = wrows[2 * w + 1];
+    }
+    for (int rl = tid; rl < nrows; rl += blockDim.x) {
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < FLAT_WAVES; ++w) {
+                const int j = rl - f[w];
+                const bool in = j >= 0 && j < n[w];
+                const float pv = part[(w * J + (in ? j : 0)) * C + cc];
+                v += in ? pv : 0.0f;
+            }
+            Y[cc * ldy_m + (int64_t)(r0 + rl) * ldy_n] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- row-tile kernel
+// Many short-lived workgroups, each owning R whole rows (R*bpr a multiple of
+// 8, so the tile is a whole number of 8-super-block steps).  The 8 waves of a
+// workgroup interleave the tile's steps (wave w takes steps w, w+8, ...), so
+// at any moment a workgroup reads adjacent 1088-byte steps and the grid as a
+// whole sweeps the matrix -- the order HBM serves best.  A wave streams its
+// steps through a ring of D register buffers (each refilled right after it
+// is consumed: D-1 steps in flight during every compute; the first D-1 fly
+// while the activations are staged or quantised into LDS).  Each lane's
+// sub-block term is summed over the 8 lanes of its super-block (DPP) and
+// parked in LDS; rows are summed at the end, in super-block order, so rows
+// may cross steps and waves freely and the result is deterministic.
+constexpr int TILE_WAVES = 8;
+
+template <int C, int D, bool kDebug, bool kFuse>
+__global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ aqs, const uint32_t* __restrict__ ads,
+    const float* __restrict__ X, int64_t sc, int64_t sk, float* __restrict__ Y, int K, int N, int64_t ldy_m,
+    int64_t ldy_n, int rows_per_wg, int32_t* __restrict__ dbg) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bpr = K / QK_K, nb = K / QK8_1;
+    int8_t* sq = reinterpret_cast<int8_t*>(lds);
+    float* sdx = reinterpret_cast<float*>(lds + (size_t)C * K);
+    float* part = sdx + C * nb;  // [C][rows_per_wg * bpr] super-block partials
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, slot = lane >> 3, ib = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nrows = min(rows_per_wg, N - r0);
+    const int n_sb = nrows * bpr;
+    const int n_steps = (n_sb + 7) >> 3;
+    const int my_n = wave < n_steps ? (n_steps - wave + TILE_WAVES - 1) / TILE_WAVES : 0;
+    const uint8_t* Wg = W + (size_t)r0 * bpr * BLOCK_BYTES;
+
+    // Only the grid's last tile can end inside a step: there the lanes past
+    // the end re-read the last super-block and are not accumulated.
+    const int last_step = n_steps - 1;
+    const int last_slot = (n_sb - 1) - 8 * last_step;
+    const uint32_t off_n = (uint32_t)slot * BLOCK_BYTES;
+    const uint32_t off_l = (uint32_t)min(slot, last_slot) * BLOCK_BYTES;
+    const uint32_t off_q = 16u * (uint32_t)ib;
+    auto load = [&](StepRegs& r, int s) {
+        const uint8_t* base = Wg + (size_t)s * (8 * BLOCK_BYTES);  // scalar
+        const uint32_t o = s == last_step ? off_l : off_n;
+        r.h = *reinterpret_cast<const v2u*>(base + o);
+        r.q = *reinterpret_cast<const v4i_a8*>(base + (o + off_q) + 8);
+    };
+
+    // Every load is unconditional (steps past this wave's last one repeat
+    // it), so the wait counts are compile-time exact.
+    StepRegs buf[D];
+    if (my_n > 0) {
+#pragma unroll
+        for (int d = 0; d < D - 1; ++d) load(buf[d], wave + TILE_WAVES * min(d, my_n - 1));
+    }
+    if (kFuse)
+        quantize_to_lds(X, sc, sk, C, K, sq, sdx, tid, blockDim.x);
+    else
+        stage_activations(aqs, ads, C, K, sq, sdx, tid, blockDim.x);
+    __syncthreads();
+
+    const int sh_lo = 4 * ib, sh_hi = 16 + 2 * ib;
+    const int sb_stride = (TILE_WAVES * 8) % bpr;  // super-block advance per own step, mod bpr
+    int u = (8 * wave) % bpr;                        // (8*s) mod bpr for the current step (wave-uniform)
+    auto compute = [&](const StepRegs& cur, int s) {
+        const int sb = 8 * s + slot;
+        const bool valid = s != last_step || slot <= last_slot;
+        int pos = u + slot;                     // position of the super-block inside its row
+        pos = pos >= bpr ? pos - bpr : pos;     // bpr >= 8 (host)
+        const int a_idx = 8 * pos + ib;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)cur.q[j], lo[j], hi[j]);
+        const int ls = (int)(((cur.h.y >> sh_lo) & 0xFu) | (((cur.h.x >> sh_hi) & 0x3u) << 4)) - 32;
+        const float dw = half_bits_to_float(cur.h.x & 0xFFFFu);
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc) {
+            const v4i* pa = reinterpret_cast<const v4i*>(sq + cc * K + a_idx * QK8_1);
+            const v4i a0 = pa[0], a1 = pa[1];
+            int sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sum = dot4(lo[j], (uint32_t)a0[j], sum);
+                sum = dot4(hi[j], (uint32_t)a1[j], sum);
+            }
+            sum = __mul24(sum, ls);
+            float t = valid ? (dw * sdx[cc * nb + a_idx]) * (float)sum : 0.0f;
+            if (kDebug && valid) {
+                const int row = sb / bpr;
+                dbg[((int64_t)cc * N + r0 + row) * nb + a_idx] = sum;
+            }
+            // sum over the 8 sub-blocks of the super-block (lanes 8*slot .. 8*slot+7)
+            t += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, t), 0xB1, 0xF, 0xF, true));
+            t += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, t), 0x4E, 0xF, 0xF, true));
+            t += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, t), 0x141, 0xF, 0xF, true));
+            if (ib == 0 && valid) part[cc * rows_per_wg * bpr + sb] = t;
+        }
+    };
+    for (int i0 = 0; i0 < my_n; i0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int i = i0 + d;
+            load(buf[(d + D - 1) % D], wave + TILE_WAVES * min(i + D - 1, my_n - 1));
+            if (i < my_n) compute(buf[d], wave + TILE_WAVES * i);
+            u += sb_stride;
+            u = u >= bpr ? u - bpr : u;
+        }
+    }
+    __syncthreads();
+    // Row sums in super-block order.
+    for (int i = tid; i < nrows * C; i += blockDim.x) {
+        const int cc = i / nrows, rl = i - cc * nrows;
+        const float* pr = part + cc * rows_per_wg * bpr + rl * bpr;
+        float v = 0.0f;
+        for (int b = 0; b < bpr; ++b) v += pr[b];
+        Y[cc * ldy_m + (int64_t)(r0 + rl) * ldy_n] = v;
+    }
+}
+
 // ---------------------------------------------------------------- launchers
 constexpr int GEMV_WAVES_PER_WG = 8;
 constexpr size_t GEMV_LDS_BUDGET = 64 * 1024;
@@ -322,6 +637,98 @@ static hipError_t launch_lds(const uint8_t* W, const int8_t* aqs, const uint32_t
     return hipGetLastError();
 }
 
+static int tuning_knob(const char* name, int def, int lo, int hi) {
+    const char* v = getenv(name);
+    if (v == nullptr) return def;
+    const int x = atoi(v);
+    return (x < lo || x > hi) ? def : x;
+}
+
+template <int C, int D>
+static hipError_t launch_flat(const uint8_t* W, const int8_t* aqs, const uint32_t* aqs_ds, const float* X,
+                              int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m, int64_t ldy_n,
+                              int32_t* dbg, hipStream_t stream) {
+    const int64_t bpr = K / QK_K, nb = K / QK8_1;
+    const int64_t g = 8 / std::gcd<int64_t, int64_t>(bpr, 8);   // rows per 8-super-block boundary
+    static const int wgs_per_cu = tuning_knob("IQ4XS_GEMV_WGS_PER_CU", 2, 1, 8);
+    const int64_t target = (int64_t)wgs_per_cu * device_cu_count();
+    const int64_t units = (N + g - 1) / g;
+    const int64_t rows_per_wg = ((units + target - 1) / target) * g;
+    const int64_t wgs = (N + rows_per_wg - 1) / rows_per_wg;
+    if (rows_per_wg * bpr * BLOCK_BYTES >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    const int64_t steps = (rows_per_wg * bpr + 7) / 8;
+    const int64_t q_max = (steps + FLAT_WAVES - 1) / FLAT_WAVES;
+    const int64_t J = (8 * q_max - 1) / bpr + 2;
+    const size_t lds = (size_t)C * K + (size_t)C * nb * 4 + (size_t)FLAT_WAVES * J * C * 4 + FLAT_WAVES * 8;
+    if (lds > GEMV_LDS_BUDGET) return hipErrorNotSupported;
+    const dim3 grid((unsigned)wgs), block(64 * FLAT_WAVES);
+#define IQ4XS_LAUNCH_FLAT(DBG, FUSE)                                                                              \
+    hipLaunchKernelGGL((gemv_flat_kernel<C, D, DBG, FUSE>), grid, block, lds, stream, W, aqs, aqs_ds, X, sc, sk, Y, \
+                       (int)K, (int)N, ldy_m, ldy_n, (int)rows_per_wg, (int)J, dbg)
+    if (X != nullptr) {
+        if (dbg) IQ4XS_LAUNCH_FLAT(true, true); else IQ4XS_LAUNCH_FLAT(false, true);
+    } else {
+        if (dbg) IQ4XS_LAUNCH_FLAT(true, false); else IQ4XS_LAUNCH_FLAT(false, false);
+    }
+#undef IQ4XS_LAUNCH_FLAT
+    return hipGetLastError();
+}
+
+// Rows per tile: a multiple of g (so a tile is a whole number of steps),
+// sized for about `tiles_per_cu` tiles per CU.
+static int64_t tile_rows(int64_t bpr, int64_t N) {
+    const int64_t g = 8 / std::gcd<int64_t, int64_t>(bpr, 8);
+    static const int tiles_per_cu = tuning_knob("IQ4XS_GEMV_TILES_PER_CU", 2, 1, 64);
+    const int64_t tiles = (int64_t)tiles_per_cu * device_cu_count();
+    const int64_t units = (N + g - 1) / g;
+    return ((units + tiles - 1) / tiles) * g;
+}
+
+template <int C, int D>
+static hipError_t launch_tile_d(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X,
+                                int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m, int64_t ldy_n,
+                                int32_t* dbg, int64_t R, hipStream_t stream) {
+    const int64_t bpr = K / QK_K, nb = K / QK8_1;
+    const int64_t wgs = (N + R - 1) / R;
+    const size_t lds = (size_t)C * K + (size_t)C * nb * 4 + (size_t)C * R * bpr * 4;
+    if (lds > GEMV_LDS_BUDGET || wgs > 0x7FFFFFFF) return hipErrorNotSupported;
+    const dim3 grid((unsigned)wgs), block(64 * TILE_WAVES);
+#define IQ4XS_LAUNCH_TILE(DBG, FUSE)                                                                              \
+    hipLaunchKernelGGL((gemv_tile_kernel<C, D, DBG, FUSE>), grid, block, lds, stream, W, aqs, ads, X, sc, sk, Y,  \
+                       (int)K, (int)N, ldy_m, ldy_n, (int)R, dbg)
+    if (X != nullptr) {
+        if (dbg) IQ4XS_LAUNCH_TILE(true, true); else IQ4XS_LAUNCH_TILE(false, true);
+    } else {
+        if (dbg) IQ4XS_LAUNCH_TILE(true, false); else IQ4XS_LAUNCH_TILE(false, false);
+    }
+#undef IQ4XS_LAUNCH_TILE
+    return hipGetLastError();
+}
+
+template <int C>
+static hipError_t launch_tile(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X, int64_t sc,
+                              int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
+                              hipStream_t stream) {
+    const int64_t bpr = K / QK_K;
+    const int64_t R = tile_rows(bpr, N);
+    if (R * bpr * BLOCK_BYTES >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    static const int depth = tuning_knob("IQ4XS_GEMV_TILE_D", 2, 2, 3);
+    if (depth == 3) return launch_tile_d<C, 3>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, R, stream);
+    return launch_tile_d<C, 2>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, R, stream);
+}
+
+template <int C>
+static hipError_t launch_flat_depth(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X,
+                                    int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m,
+                                    int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    static const int depth = tuning_knob("IQ4XS_GEMV_DEPTH", 3, 2, 4);
+    switch (depth) {
+        case 2: return launch_flat<C, 2>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        case 4: return launch_flat<C, 4>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+        default: return launch_flat<C, 3>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+    }
+}
+
 // X == nullptr: planar Q8_1 activations (aqs, ads); otherwise fp32 X quantised
 // in the prologue (fused; returns hipErrorNotSupported when it does not fit).
 template <int C>
@@ -330,7 +737,13 @@ static hipError_t launch_cols(const uint8_t* W, const int8_t* aqs, const uint32_
                               hipStream_t stream) {
     const int64_t bpr = K / QK_K;
     hipError_t err = hipErrorNotSupported;
-    if (K <= (1 << 24) && N < (1 << 30)) {
+    static const int kind = tuning_knob("IQ4XS_GEMV_KIND", 2, 0, 2);  // 0 items, 1 flat, 2 tile
+    const bool fits = K <= (1 << 24) && N < (1 << 30);
+    if (fits && bpr >= 8 && kind == 2)
+        err = launch_tile<C>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+    if (err == hipErrorNotSupported && fits && bpr >= 8 && kind >= 1)
+        err = launch_flat_depth<C>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
+    if (err == hipErrorNotSupported && fits) {
         if (bpr % 8 == 4)
             err = launch_lds<C, 2>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
         else
