@@ -66,9 +66,11 @@ int quantize_row_q8_1_gpu(const float* x, void* y, int64_t K, void* stream);
 int quantize_row_q8_1_batched_gpu(const float* X, void* Y, int64_t K, int64_t M, void* stream);
 
 /* Replaces gemv_iq4xs_stock_dp4a_gpu, real_stock_dp4a_comparator.hip:480-503:
- * y[N] = W x (x quantised to Q8_1 first).  The Q8_1 scratch comes from the
- * device's stream-ordered pool (hipMallocAsync/hipFreeAsync on `stream`): no
- * device-wide synchronisation, unlike the reference's hipMalloc/hipFree. */
+ * y[N] = W x (x quantised to Q8_1 first).  For K <= 6144 the quantisation runs
+ * inside the GEMV kernel (one launch, no scratch); otherwise the Q8_1 scratch
+ * comes from the device's stream-ordered pool (hipMallocAsync/hipFreeAsync on
+ * `stream`): no device-wide synchronisation, unlike the reference's
+ * hipMalloc/hipFree. */
 int gemv_iq4xs_stock_dp4a_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
 
 /* Replaces the C-linkage gemv_iq4xs_dp4a_coop_gpu, impl_gemv_dp4a_gfx1100.hip:332-341
@@ -122,7 +124,8 @@ int iq4xs_quantize_q8_1(const float* X, int64_t K, int64_t M, int layout, void* 
 int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,
                        int path, void* stream);
 
-/* Quantise + multiply in one call. */
+/* Quantise + multiply in one call.  For M == 1 and K <= 6144 the quantisation
+ * runs inside the GEMV kernel and ws is not written (it is still validated). */
 int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
                   size_t ws_bytes, void* stream);
 
