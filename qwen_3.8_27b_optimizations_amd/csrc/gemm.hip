@@ -5,8 +5,12 @@
 // where sumi is the exact int32 dot of a 32-weight sub-block with the
 // matching Q8_1 block.
 //
-// MI355X mapping.  A workgroup (4 waves) owns a 64-row x 64-token output
-// tile and walks K one 256-weight super-block at a time:
+// Two kernels share this scheme (the launcher picks one per shape):
+// gemm_iq4xs_db_kernel (128x128 tile, 16 waves, double-buffered LDS) and
+// gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves, four per CU).
+//
+// MI355X mapping (64x64 kernel).  A workgroup (4 waves) owns a 64-row x
+// 64-token output tile and walks K one 256-weight super-block at a time:
 //   1. the 64 weight rows' super-blocks are decoded (v_perm codebook lookup,
 //      decode_codes_x)
 //      straight into int8 LDS tiles, the per-sub-block weight scales
@@ -18,6 +22,8 @@
 // LDS rows are 256 bytes; the 16-byte chunk index is XORed with (row & 15)
 // so the 32 lanes that read one k-chunk of 32 different rows hit 16
 // distinct chunk positions (no bank conflicts from the 256-byte row stride).
+#include <stdlib.h>
+
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 
@@ -104,12 +110,16 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
             const int ch = 2 * s + (lane >> 5);
             const v4i a = *reinterpret_cast<const v4i*>(sW + lds_swz(ra, ch));
             const v4i b = *reinterpret_cast<const v4i*>(sX + lds_swz(rb, ch));
-            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
+            v4f sa[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                sa[j] = *reinterpret_cast<const v4f*>(&sA[s][32 * wn + 8 * j + 4 * (lane >> 5)]);
             const float bx = sB[s][rb];
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int i = 32 * wn + mfma_c_row(e, lane);
-                acc[e] += (sA[s][i] * bx) * (float)c[e];
+                acc[e] += (sa[e >> 2][e & 3] * bx) * (float)c[e];
                 if (kDebug) {
                     const int64_t n = n0 + i, m = m0 + rb;
                     if (n < N && m < M) dbg[(m * N + n) * nb + kb * 8 + s] = c[e] * sL[s][i];
@@ -128,8 +138,204 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
     }
 }
 
+// ---------------------------------------------------------------- 128 x 128 double-buffered kernel
+// 16 waves own a 128-row x 128-token tile; wave w computes the 32x32 block at
+// rows 32*(w&3), tokens 32*(w>>2) (one MFMA per 32-wide sub-block).  LDS holds
+// two stages; while the waves run the MFMAs and the scale epilogue of
+// super-block kb from one stage, the global loads of super-block kb+1 are in
+// flight, and they are decoded into the other stage afterwards: one barrier
+// per super-block.  Rows are padded to 272 bytes instead of swizzled: the 16
+// lanes of a ds_read_b128 phase still hit 16 distinct 16-byte bank groups
+// (272*r mod 256 = 16*r), and the address of sub-block s is a constant
+// offset from sub-block 0 (no per-sub-block address arithmetic).
+constexpr int G2_BN = 128, G2_BM = 128, G2_THREADS = 1024;
+constexpr int G2_ROW = 272;                                  // padded LDS row (256 codes + 16)
+constexpr int G2_W_BYTES = G2_BN * G2_ROW, G2_X_BYTES = G2_BM * G2_ROW;
+constexpr int G2_SA_OFF = G2_W_BYTES + G2_X_BYTES;         // float [8][128]
+constexpr int G2_SB_OFF = G2_SA_OFF + 8 * G2_BN * 4;        // float [8][128]
+constexpr int G2_SL_OFF = G2_SB_OFF + 8 * G2_BM * 4;        // int8  [8][128] (debug only)
+constexpr int G2_STAGE = G2_SL_OFF;                          // bytes per stage without the debug table
+constexpr int G2_STAGE_DBG = G2_SL_OFF + 8 * G2_BN;
+
+struct GemmPref {
+    v4i wq;
+    v2u wh;
+    v4i x[2];
+    uint32_t ds;
+};
+
+template <bool kDebug>
+__global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t* __restrict__ W,
+                                                                   const int8_t* __restrict__ aqs,
+                                                                   const uint32_t* __restrict__ ads,
+                                                                   float* __restrict__ Y, int64_t K, int64_t N,
+                                                                   int64_t M, int64_t ldy_m, int64_t ldy_n,
+                                                                   int32_t* __restrict__ dbg) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int kStage = kDebug ? G2_STAGE_DBG : G2_STAGE;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave & 3, wm = wave >> 2;
+    const int64_t n0 = (int64_t)blockIdx.x * G2_BN;
+    const int64_t m0 = (int64_t)blockIdx.y * G2_BM;
+    const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
+
+    // this thread's share of a super-block's loads (rows / tokens past the end
+    // are clamped to the last one; their results are never stored)
+    const int wr = tid >> 3, wsb = tid & 7;  // weight row, sub-block
+    const uint8_t* wrow = W + ((n0 + wr < N) ? n0 + wr : N - 1) * row_bytes;
+    int xr[2], xc[2];
+    const int8_t* xrow[2];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int p = tid + G2_THREADS * it;
+        xr[it] = p >> 4;
+        xc[it] = p & 15;
+        xrow[it] = aqs + ((m0 + xr[it] < M) ? m0 + xr[it] : M - 1) * K + 16 * xc[it];
+    }
+    const int dr = tid >> 3, ds_s = tid & 7;  // token, sub-block of the d word
+    const uint32_t* drow = ads + ((m0 + dr < M) ? m0 + dr : M - 1) * nb + ds_s;
+
+    auto load = [&](GemmPref& g, int64_t kb) {
+        const uint8_t* blk = wrow + kb * BLOCK_BYTES;
+        g.wh = *reinterpret_cast<const v2u*>(blk);
+        g.wq = *reinterpret_cast<const v4i_a8*>(blk + 8 + 16 * wsb);
+#pragma unroll
+        for (int it = 0; it < 2; ++it) g.x[it] = *reinterpret_cast<const v4i*>(xrow[it] + kb * QK_K);
+        g.ds = drow[kb * 8];
+    };
+    auto store = [&](const GemmPref& g, int stage) {
+        uint8_t* base = lds + stage * kStage;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)g.wq[j], lo[j], hi[j]);
+        int8_t* wdst = reinterpret_cast<int8_t*>(base) + wr * G2_ROW + 32 * wsb;
+        *reinterpret_cast<v4i*>(wdst) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+        *reinterpret_cast<v4i*>(wdst + 16) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        const int ls = subblock_ls(g.wh.x, g.wh.y, wsb) - 32;
+        reinterpret_cast<float*>(base + G2_SA_OFF)[wsb * G2_BN + wr] = half_bits_to_float(g.wh.x & 0xFFFFu) * (float)ls;
+        if (kDebug) reinterpret_cast<int8_t*>(base + G2_SL_OFF)[wsb * G2_BN + wr] = (int8_t)ls;
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+            *reinterpret_cast<v4i*>(base + G2_W_BYTES + xr[it] * G2_ROW + 16 * xc[it]) = g.x[it];
+        reinterpret_cast<float*>(base + G2_SB_OFF)[ds_s * G2_BM + dr] = half_bits_to_float(g.ds & 0xFFFFu);
+    };
+
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    const int ra = 32 * wn + (lane & 31);
+    const int rb = 32 * wm + (lane & 31);
+    const int half = lane >> 5;  // k = 16*half .. +15 of each 32-wide sub-block
+
+    GemmPref g;
+    load(g, 0);
+    store(g, 0);
+    __syncthreads();
+    for (int64_t kb = 0; kb < bpr; ++kb) {
+        const int cur = (int)(kb & 1);
+        const bool more = kb + 1 < bpr;
+        if (more) load(g, kb + 1);  // in flight during the MFMA phase
+        const uint8_t* base = lds + cur * kStage;
+        const int8_t* pa = reinterpret_cast<const int8_t*>(base) + ra * G2_ROW + 16 * half;
+        const int8_t* pb = reinterpret_cast<const int8_t*>(base + G2_W_BYTES) + rb * G2_ROW + 16 * half;
+        const float* pA = reinterpret_cast<const float*>(base + G2_SA_OFF) + 32 * wn + 4 * half;
+        const float* pB = reinterpret_cast<const float*>(base + G2_SB_OFF) + rb;
+#pragma unroll 2
+        for (int s = 0; s < 8; ++s) {
+            const v4i a = *reinterpret_cast<const v4i*>(pa + 32 * s);
+            const v4i b = *reinterpret_cast<const v4i*>(pb + 32 * s);
+            // row scales of this lane's 16 elements: rows 8j + 4*half + 0..3
+            v4f sa[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sa[j] = *reinterpret_cast<const v4f*>(pA + s * G2_BN + 8 * j);
+            const float bx = pB[s * G2_BM];
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                acc[e] += (sa[e >> 2][e & 3] * bx) * (float)c[e];
+                if (kDebug) {
+                    const int i = 32 * wn + mfma_c_row(e, lane);
+                    const int8_t* sL = reinterpret_cast<const int8_t*>(base + G2_SL_OFF);
+                    const int64_t m = m0 + rb;
+                    if (m < M && n0 + i < N) dbg[(m * N + n0 + i) * nb + kb * 8 + s] = c[e] * (int)sL[s * G2_BN + i];
+                }
+            }
+        }
+        if (more) store(g, cur ^ 1);
+        __syncthreads();
+    }
+
+    const int64_t m = m0 + rb;
+    if (m < M) {
+        float* yrow = Y + m * ldy_m;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t n = n0 + 32 * wn + mfma_c_row(e, lane);
+            if (n < N) yrow[n * ldy_n] = acc[e];
+        }
+    }
+}
+
+static int gemm_kind() {
+    static const int kind = []() {
+        const char* v = getenv("IQ4XS_GEMM_KIND");  // tuning override: 0 = 64x64, 1 = 128x128
+        return v ? atoi(v) : -1;
+    }();
+    return kind;
+}
+
+static int gemm_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// The 128x128 kernel runs one workgroup per CU and is ~1.2x faster per tile;
+// the 64x64 kernel (four per CU) wins when big tiles leave CUs idle: fewer
+// tiles than ~9/16 of the CUs, or a last round that is mostly empty
+// (thresholds from measurements on the 27B-class shapes at M = 512 / 2048).
+static bool use_big_tiles(int64_t N, int64_t M) {
+    const int k = gemm_kind();
+    if (k == 0 || k == 1) return k == 1;
+    const int64_t cus = gemm_cu_count();
+    const int64_t tiles = ((N + G2_BN - 1) / G2_BN) * ((M + G2_BM - 1) / G2_BM);
+    if (tiles < cus * 9 / 16) return false;
+    const int64_t rounds = tiles / cus, rest = tiles % cus;
+    return !(rounds >= 1 && rounds < 4 && rest > 0 && rest <= cus / 4);
+}
+
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    if (use_big_tiles(N, M)) {
+        const int64_t gx = (N + G2_BN - 1) / G2_BN;
+        const int64_t gy = (M + G2_BM - 1) / G2_BM;
+        if (gx > 0x7FFFFFFF || gy > 65535) return hipErrorInvalidConfiguration;
+        const size_t lds = 2 * (size_t)(dbg ? G2_STAGE_DBG : G2_STAGE);
+        static const bool attrs = []() {
+            // two stages exceed the default dynamic-LDS cap; gfx950 has 160 KB per CU
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_iq4xs_db_kernel<false>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 2 * G2_STAGE);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_iq4xs_db_kernel<true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 2 * G2_STAGE_DBG);
+            return true;
+        }();
+        (void)attrs;
+        if (dbg)
+            hipLaunchKernelGGL(gemm_iq4xs_db_kernel<true>, dim3((unsigned)gx, (unsigned)gy), dim3(G2_THREADS), lds,
+                               stream, W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg);
+        else
+            hipLaunchKernelGGL(gemm_iq4xs_db_kernel<false>, dim3((unsigned)gx, (unsigned)gy), dim3(G2_THREADS), lds,
+                               stream, W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg);
+        return hipGetLastError();
+    }
     const int64_t gx = (N + GEMM_BN - 1) / GEMM_BN;
     const int64_t gy = (M + GEMM_BM - 1) / GEMM_BM;
     if (gx > 0x7FFFFFFF || gy > 65535) return hipErrorInvalidConfiguration;

@@ -34,7 +34,6 @@
 
 namespace iq4xs {
 
-typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- fallback
 template <int C, bool kDebug>

@@ -36,6 +36,7 @@ struct block_q8_1 {
 static_assert(sizeof(block_q8_1) == Q8_1_BYTES, "block_q8_1 is 36 bytes");
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 // 16-byte vector whose address is only known to be 8-byte aligned (the qs of
