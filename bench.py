@@ -19,6 +19,8 @@ roofline  the GEMV kernel alone, on prequantised Q8_1 activations: a graph of
 extra     bs = 2, 4, 8 (the same GEMV-only measurement with 1 % x20
           outliers) and the int8-MFMA GEMM at M = 512 and 2048 (2*M*N*K over
           the average of back-to-back launches rotated over the layer copies).
+model_stream  64 distinct layers resident (12.30 GB): one bs=1 token (448
+          calls, graph) and one bs=512 pass (quantise + GEMM per call).
 cpu_baseline  the reference's own FP64 oracle (kernels/matmul_iq4xs/ref_cpu.cpp,
           compiled into oracle/_ref) -- or this repository's restatement where
           that is absent -- on one host core, on a bounded sample.
@@ -59,6 +61,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--model-layers", type=int, default=64,
+                    help="whole-model weight stream: distinct resident layers (0 = skip)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (4 times): the known-size reference that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -133,6 +137,66 @@ def capture(torch, stream, fn, use_graph: bool):
     except Exception as e:  # capture unsupported: fall back to eager launches
         print(f"[bench] graph capture failed ({e}); timing eager launches", file=sys.stderr)
         return fn, "eager"
+
+
+def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
+    """`--model-layers` distinct layers of the seven projections resident at
+    once (64 layers = 12.30 GB).  bs=1: one token = every layer's seven calls
+    in order on one stream (each launch waits for the previous one, as a
+    layer-to-layer data chain would; the inputs stay fixed because chaining
+    the synthetic outputs would overflow the fp16 Q8_1 scale without the
+    model's normalisation layers).  bs=512: the same layers as M=512 GEMMs
+    (quantise + GEMM per call)."""
+    s = stream.cuda_stream
+    dev = torch.device("cuda:0")
+    weights = []
+    for l in range(args.model_layers):
+        row = []
+        for i, (_, K, N) in enumerate(SHAPES):
+            W = torch.empty(N * K // 256 * 136, dtype=torch.uint8, device=dev)
+            L.check("iq4xs_fill_synthetic_weights", W.data_ptr(), N * K // 256, 42, (1 << 40) + ((l * 7 + i) << 24), s)
+            row.append(W)
+        weights.append(row)
+    layer_bytes = sum(gemv_bytes(K, N) for _, K, N in SHAPES)
+    total_w = sum(N * K // 256 * 136 for _, K, N in SHAPES) * args.model_layers
+    xs = [pkg.synthetic_activations(K, seed=700 + i, device=dev) for i, (_, K, _) in enumerate(SHAPES)]
+    ys = [torch.empty(N, device=dev) for (_, _, N) in SHAPES]
+    wss = [torch.empty(L.iq4xs_workspace_bytes(K, 1), dtype=torch.uint8, device=dev) for (_, K, _) in SHAPES]
+    torch.cuda.synchronize()
+
+    def token() -> None:
+        for l in range(args.model_layers):
+            for i, (_, K, N) in enumerate(SHAPES):
+                L.check("iq4xs_mul_mat", weights[l][i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), K, N, 1,
+                        pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
+
+    run, launch = capture(torch, stream, token, use_graph)
+    timer(run, 2)
+    us = timer(run, 8) / 8
+    out = {"layers": args.model_layers, "weight_bytes": total_w,
+           "bs1": {"us_per_token": round(us, 1), "GBps": round(layer_bytes * args.model_layers / (us * 1e-6) / 1e9, 1),
+                   "frac_of_hbm_peak": round(layer_bytes * args.model_layers / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                   "tokens_per_s_upper_bound": round(1e6 / us, 1), "launch": launch}}
+    del run, xs, ys, wss
+    M = 512
+    Xs = [pkg.synthetic_activations(K * M, seed=800 + i, device=dev) for i, (_, K, _) in enumerate(SHAPES)]
+    Ys = [torch.empty((M, N), device=dev) for (_, _, N) in SHAPES]
+    Ws = [torch.empty(L.iq4xs_workspace_bytes(K, M), dtype=torch.uint8, device=dev) for (_, K, _) in SHAPES]
+
+    def prefill() -> None:
+        for l in range(args.model_layers):
+            for i, (_, K, N) in enumerate(SHAPES):
+                L.check("iq4xs_mul_mat", weights[l][i].data_ptr(), Xs[i].data_ptr(), Ys[i].data_ptr(), K, N, M,
+                        pkg.LAYOUT_MK, Ws[i].data_ptr(), Ws[i].numel(), s)
+
+    prefill()
+    torch.cuda.synchronize()
+    us = timer(prefill, 1)
+    ops = sum(2 * M * N * K for _, K, N in SHAPES) * args.model_layers
+    out["bs512"] = {"ms_per_pass": round(us / 1e3, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+                    "frac_of_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+                    "tokens_per_s": round(M / (us * 1e-6), 1), "includes": "Q8_1 quantisation of every call"}
+    return out
 
 
 def main() -> int:
@@ -258,6 +322,13 @@ def main() -> int:
         tops = ops / (us_sum * 1e-6) / 1e12
         gemm[str(M)] = {"tops": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4), "per_shape_us": per_shape}
 
+    # ---- whole-model weight stream (64 distinct layers resident) -----------
+    model = None
+    if args.model_layers:
+        del layers
+        torch.cuda.synchronize()
+        model = model_stream(torch, pkg, L, stream, timer, args, use_graph)
+
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     out = {
@@ -285,6 +356,7 @@ def main() -> int:
                      "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps},
         "small_batch_gemv": small,
         "gemm": {"peak_tops": INT8_PEAK_TOPS, "kernel": "gemm_iq4xs_mfma_kernel", "by_M": gemm},
+        "model_stream": model,
         "cpu_baseline": cpu,
         "host": platform.node(),
     }

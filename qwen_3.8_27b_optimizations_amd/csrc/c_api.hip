@@ -2,6 +2,8 @@
 // Argument checks mirror the reference launchers (hipErrorInvalidValue for
 // null pointers and bad shapes, real_stock_dp4a_comparator.hip:487,513;
 // impl_gemv_dp4a_gfx1100.hip:299-300) and run before anything is launched.
+#include <stdlib.h>
+
 #include <mutex>
 #include <vector>
 
@@ -74,7 +76,15 @@ hipError_t mul_mat_planar(const uint8_t* W, const void* ws, float* Y, int64_t K,
 // (and for M > 1) a separate quantiser launch is cheaper.
 constexpr int64_t FUSED_MAX_K = 6144;
 
-bool prefer_fused(int64_t K, int64_t M) { return M == 1 && K <= FUSED_MAX_K; }
+int64_t fused_max_k() {
+    static const int64_t v = []() -> int64_t {
+        const char* e = getenv("IQ4XS_FUSED_MAX_K");  // tuning override
+        return e ? atoll(e) : FUSED_MAX_K;
+    }();
+    return v;
+}
+
+bool prefer_fused(int64_t K, int64_t M) { return M == 1 && K <= fused_max_k(); }
 
 hipError_t mul_mat_fused(const uint8_t* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
                          int32_t* dbg, hipStream_t stream) {

@@ -170,39 +170,41 @@ __device__ inline void stage_activations(const int8_t* __restrict__ aqs, const u
 // the dot uses the fp16-truncated d exactly as the planar path does.  Loads of
 // up to four rounds are issued before any of them is used, so the prologue
 // costs about one memory latency rather than one per round.
-__device__ inline void quantize_to_lds(const float* __restrict__ X, int64_t sc, int64_t sk, int C, int K, int8_t* sq,
+template <int C>
+__device__ inline void quantize_to_lds(const float* __restrict__ X, int64_t sc, int64_t sk, int K, int8_t* sq,
                                        float* sdx, int tid, int nthreads) {
     constexpr int U = 4;
     const int nb = K / QK8_1;
-    const int tasks = C * nb * 8;  // a multiple of 64 (K % 256 == 0): 8-lane groups and waves stay whole
-    for (int t0 = tid; t0 < tasks; t0 += U * nthreads) {
-        float x[U][4];
+    const int tasks = nb * 8;  // per column; a multiple of 64 (K % 256 == 0): 8-lane groups and waves stay whole
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = t0 + u * nthreads;
-            if (t < tasks) {
-                const int blk = t >> 3, j = t & 7;
-                const int cc = blk / nb, ib = blk - cc * nb;
-                const float* p = X + cc * sc + (int64_t)(ib * QK8_1 + j) * sk;
-                x[u][0] = p[0];
-                x[u][1] = p[8 * sk];
-                x[u][2] = p[16 * sk];
-                x[u][3] = p[24 * sk];
+    for (int cc = 0; cc < C; ++cc) {
+        const float* Xc = X + cc * sc;
+        for (int t0 = tid; t0 < tasks; t0 += U * nthreads) {
+            float x[U][4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int t = t0 + u * nthreads;
+                if (t < tasks) {
+                    const float* p = Xc + (int64_t)((t >> 3) * QK8_1 + q8_lane_elem(t & 7)) * sk;
+                    x[u][0] = p[0];
+                    x[u][1] = p[8 * sk];
+                    x[u][2] = p[16 * sk];
+                    x[u][3] = p[24 * sk];
+                }
             }
-        }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = t0 + u * nthreads;
-            if (t < tasks) {
-                const int blk = t >> 3, j = t & 7;
-                const int cc = blk / nb, ib = blk - cc * nb;
-                const Q8Block8 b = quantize_block8(x[u][0], x[u][1], x[u][2], x[u][3]);
-                int8_t* o = sq + cc * K + ib * QK8_1 + j;
-                o[0] = (int8_t)b.q0;
-                o[8] = (int8_t)b.q1;
-                o[16] = (int8_t)b.q2;
-                o[24] = (int8_t)b.q3;
-                if (j == 0) sdx[blk] = half_bits_to_float(b.ds & 0xFFFFu);
+            for (int u = 0; u < U; ++u) {
+                const int t = t0 + u * nthreads;
+                if (t < tasks) {
+                    const int ib = t >> 3, j = q8_lane_elem(t & 7);
+                    const Q8Block8 b = quantize_block8(x[u][0], x[u][1], x[u][2], x[u][3]);
+                    int8_t* o = sq + cc * K + ib * QK8_1 + j;
+                    o[0] = (int8_t)b.q0;
+                    o[8] = (int8_t)b.q1;
+                    o[16] = (int8_t)b.q2;
+                    o[24] = (int8_t)b.q3;
+                    if (j == 0) sdx[cc * nb + ib] = half_bits_to_float(b.ds & 0xFFFFu);
+                }
             }
         }
     }
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(const uint8_t* __restrict
     StepRegs A, B;
     if (total > 0) load_step<IR>(A, W, g, item, 0, slot, ib);  // first loads fly during the prologue
     if (kFuse)
-        quantize_to_lds(X, sc, sk, C, K, sq, sdx, tid, blockDim.x);
+        quantize_to_lds<C>(X, sc, sk, K, sq, sdx, tid, blockDim.x);
     else
         stage_activations(aqs, ads, C, K, sq, sdx, tid, blockDim.x);
     __syncthreads();
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(64 * FLAT_WAVES) void gemv_flat_kernel(
         for (int d = 0; d < D - 1; ++d) load(buf[d], min(s_a + d, s_b - 1));
     }
     if (kFuse)
-        quantize_to_lds(X, sc, sk, C, K, sq, sdx, tid, blockDim.x);
+        quantize_to_lds<C>(X, sc, sk, K, sq, sdx, tid, blockDim.x);
     else
         stage_activations(aqs, ads, C, K, sq, sdx, tid, blockDim.x);
     __syncthreads();
@@ -531,15 +533,19 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
 #pragma unroll
         for (int d = 0; d < D - 1; ++d) load(buf[d], wave + TILE_WAVES * min(d, my_n - 1));
     }
+    // (8*s) mod bpr of this wave's current step, and its advance per own
+    // step (64 super-blocks) mod bpr; bpr >= 8, so a few subtractions do.
+    int u = 8 * wave;
+    while (u >= bpr) u -= bpr;
+    int sb_stride = TILE_WAVES * 8;
+    while (sb_stride >= bpr) sb_stride -= bpr;
     if (kFuse)
-        quantize_to_lds(X, sc, sk, C, K, sq, sdx, tid, blockDim.x);
+        quantize_to_lds<C>(X, sc, sk, K, sq, sdx, tid, blockDim.x);
     else
         stage_activations(aqs, ads, C, K, sq, sdx, tid, blockDim.x);
     __syncthreads();
 
     const int sh_lo = 4 * ib, sh_hi = 16 + 2 * ib;
-    const int sb_stride = (TILE_WAVES * 8) % bpr;  // super-block advance per own step, mod bpr
-    int u = (8 * wave) % bpr;                        // (8*s) mod bpr for the current step (wave-uniform)
     auto compute = [&](const StepRegs& cur, int s) {
         const int sb = 8 * s + slot;
         const bool valid = s != last_step || slot <= last_slot;
@@ -585,13 +591,23 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
         }
     }
     __syncthreads();
-    // Row sums in super-block order.
-    for (int i = tid; i < nrows * C; i += blockDim.x) {
-        const int cc = i / nrows, rl = i - cc * nrows;
-        const float* pr = part + cc * rows_per_wg * bpr + rl * bpr;
-        float v = 0.0f;
-        for (int b = 0; b < bpr; ++b) v += pr[b];
-        Y[cc * ldy_m + (int64_t)(r0 + rl) * ldy_n] = v;
+    // Row sums: 16 lanes (one DPP row) per output row; lane g sums partials
+    // g, g+16, ... in order, then a fixed DPP tree adds the 16 lanes.  Every
+    // lane of a DPP row takes the same branches.
+    const int grp = tid >> 4, gl = tid & 15;
+    const int n_grp = blockDim.x >> 4;
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) {
+        for (int rl = grp; rl < nrows; rl += n_grp) {
+            const float* pr = part + cc * rows_per_wg * bpr + rl * bpr;
+            float v = 0.0f;
+            for (int b = gl; b < bpr; b += 16) v += pr[b];
+            v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+            v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+            v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+            v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+            if (gl == 0) Y[cc * ldy_m + (int64_t)(r0 + rl) * ldy_n] = v;
+        }
     }
 }
 

@@ -6,18 +6,23 @@
 // sum = pairwise tree x[t]+x[t+16], +8, +4, +2, +1; d = amax/127 (IEEE);
 // q = amax ? (int8)roundf(x/d) : 0; ds = {rtz-fp16(d), rtz-fp16(sum)}.
 //
-// Lane j (0..7) of a group holds x[j], x[j+8], x[j+16], x[j+24]: the +16 and
-// +8 levels of the tree are in-lane, the +4/+2/+1 levels are ds_swizzle xor
-// steps inside the group.  Callers keep whole 8-lane groups active together.
+// Lane L (0..7) of a group holds x[j], x[j+8], x[j+16], x[j+24] with
+// j = q8_lane_elem(L) = L for L < 4 and 11 - L for L >= 4: the +16 and +8
+// levels of the tree are in-lane, and with lanes 4..7 reversed the +4, +2
+// and +1 levels are exactly DPP row_half_mirror (L <-> 7-L), quad_perm xor 2
+// and quad_perm xor 1 -- VALU modifiers, no LDS round trip.  Callers keep
+// whole, 8-aligned lane groups active together.
 #pragma once
 
 #include "iq4xs_device.h"
 
 namespace iq4xs {
 
-template <int X>
-__device__ inline float swizzle_xor(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (X << 10)));
+__host__ __device__ constexpr int q8_lane_elem(int L) { return L < 4 ? L : 11 - L; }
+
+template <int CTRL>
+__device__ inline float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
 // roundf(x / d) with IEEE semantics, for |x| <= 127 * d.  p = x * rcp(d) lies
@@ -43,12 +48,12 @@ struct Q8Block8 {
 __device__ inline Q8Block8 quantize_block8(float x0, float x1, float x2, float x3) {
     float a = fmaxf(fmaxf(fabsf(x0), fabsf(x2)), fmaxf(fabsf(x1), fabsf(x3)));
     float s = (x0 + x2) + (x1 + x3);
-    a = fmaxf(a, swizzle_xor<4>(a));
-    s = s + swizzle_xor<4>(s);
-    a = fmaxf(a, swizzle_xor<2>(a));
-    s = s + swizzle_xor<2>(s);
-    a = fmaxf(a, swizzle_xor<1>(a));
-    s = s + swizzle_xor<1>(s);
+    a = fmaxf(a, dpp_f32<0x141>(a));  // row_half_mirror: element t with t + 4
+    s = s + dpp_f32<0x141>(s);
+    a = fmaxf(a, dpp_f32<0x4E>(a));   // quad_perm [2,3,0,1]: t with t + 2
+    s = s + dpp_f32<0x4E>(s);
+    a = fmaxf(a, dpp_f32<0xB1>(a));   // quad_perm [1,0,3,2]: t with t + 1
+    s = s + dpp_f32<0xB1>(s);
     const float d = a / 127.0f;
     Q8Block8 out{0, 0, 0, 0, float_to_half_bits_rtz(d) | (float_to_half_bits_rtz(s) << 16)};
     if (a != 0.0f) {

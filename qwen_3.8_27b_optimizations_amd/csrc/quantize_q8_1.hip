@@ -8,8 +8,8 @@
 //
 // MI355X mapping:
 //   layout MK (X[m*K+k], ggml src1 and bs=1 vectors): eight lanes per block,
-//     four elements and four divisions per lane, tree finished with
-//     ds_swizzle xor steps (quantize_q8_1_rows_kernel);
+//     four elements and four divisions per lane, tree finished with DPP
+//     steps (quantize_q8_1_rows_kernel);
 //   layout KM (X[k*M+m], standalone API): one lane per block, lanes walk
 //     consecutive columns m so each of the 32 loads of a wave covers 64
 //     consecutive floats; the tree is evaluated in registers.
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void quantize_q8_1_rows_kernel(const float* __
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = t >> 3;
     if (blk >= nb * M) return;
-    const int j = (int)(t & 7);
+    const int j = q8_lane_elem((int)(t & 7));
     const int64_t m = blk / nb, ib = blk - m * nb;
     const float* p = X + m * K + ib * QK8_1 + j;
     const Q8Block8 b = quantize_block8(p[0], p[8], p[16], p[24]);
