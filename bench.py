@@ -16,6 +16,7 @@ roofline  the GEMV kernel alone, on prequantised Q8_1 activations: a graph of
           the seven GEMV launches of every layer copy (no quantiser), timed
           with HIP events on the launch stream; achieved = the same
           algorithmic bytes / average launch duration.
+dequant   IQ4_XS -> fp32 (dequant_iq4xs_gpu) over the seven weight matrices.
 extra     bs = 2, 4, 8 (the same GEMV-only measurement with 1 % x20
           outliers) and the int8-MFMA GEMM at M = 512 and 2048 (2*M*N*K over
           the average of back-to-back launches rotated over the layer copies).
@@ -297,6 +298,25 @@ def main() -> int:
                          "us_per_layer": round(us / args.layers, 2)}
         del X, wsb, yb, brun
 
+    # ---- IQ4_XS -> fp32 dequantiser (136 B in, 1024 B out per super-block) --
+    dq_bytes, dq_us = 0, 0.0
+    for i, (_, K, N) in enumerate(SHAPES):
+        nblk = N * K // 256
+        out = torch.empty(nblk * 256, dtype=torch.float32, device=dev)
+        L.check("dequant_iq4xs_gpu", layers[0][i].data_ptr(), out.data_ptr(), nblk, 64, s)
+        ctr = [1]
+
+        def dq():
+            L.check("dequant_iq4xs_gpu", layers[ctr[0] % args.layers][i].data_ptr(), out.data_ptr(), nblk, 64, s)
+            ctr[0] += 1
+
+        dq_us += timer(dq, 4) / 4
+        dq_bytes += nblk * (136 + 1024)
+        del out
+    dequant = {"GBps": round(dq_bytes / (dq_us * 1e-6) / 1e9, 1),
+               "frac_of_hbm_peak": round(dq_bytes / (dq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+               "bytes_per_superblock": "136 read + 1024 written", "shapes": "the seven projections of one layer"}
+
     # ---- GEMM at M = 512 / 2048 on the same shapes -------------------------
     gemm = {}
     for M in args.gemm_m:
@@ -356,6 +376,7 @@ def main() -> int:
                      "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps},
         "small_batch_gemv": small,
         "gemm": {"peak_tops": INT8_PEAK_TOPS, "kernel": "gemm_iq4xs_mfma_kernel", "by_M": gemm},
+        "dequant": dequant,
         "model_stream": model,
         "cpu_baseline": cpu,
         "host": platform.node(),

@@ -83,6 +83,12 @@ int gemv_iq4xs_dp4a_coop_gpu(const void* W, const float* x, float* y, int64_t K,
 int gemm_iq4xs_stock_dp4a_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
                               void* stream);
 
+/* Replaces dequant_iq4xs_gpu, kernels/demo_iq4xs_dequant/impl.hip:51-69:
+ * n_blocks super-blocks -> 256*n_blocks fp32 weights, bit-identical to the
+ * reference's CPU dequantiser (ref_cpu.cpp:6-27).  warp_size is accepted for
+ * signature compatibility (32 or 64); the kernel always runs wave64. */
+int dequant_iq4xs_gpu(const void* src, float* dst, int64_t n_blocks, int warp_size, void* stream);
+
 /* ============================ ggml mul_mat boundary ============================ */
 
 /* Replaces custom_gemv_iq4xs_can_handle, patch:274-277.  True for

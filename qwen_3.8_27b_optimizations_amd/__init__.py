@@ -48,6 +48,7 @@ SIGNATURES = {
     "gemv_iq4xs_stock_dp4a_gpu": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "gemv_iq4xs_dp4a_coop_gpu": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "gemm_iq4xs_stock_dp4a_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "dequant_iq4xs_gpu": (_INT, [_P, _P, _I64, _INT, _P]),
     "custom_gemv_iq4xs_can_handle": (ctypes.c_bool, [_I64, _I64, _I64, _INT]),
     "custom_gemv_iq4xs_dispatch": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "custom_gemm_iq4xs_can_handle": (ctypes.c_bool, [_I64, _I64, _I64, _INT]),
@@ -195,6 +196,16 @@ def subblock_sums(W, ws, K: int, N: int, M: int, path: int):
     lib().check("iq4xs_subblock_sums", W.data_ptr(), ws.data_ptr(), S.data_ptr(), Y.data_ptr(), K, N, M, path,
                 _stream(torch))
     return S, Y
+
+
+def dequant(W, n_blocks: int, out=None):
+    """IQ4_XS super-blocks -> fp32 weights [n_blocks * 256]."""
+    torch = _torch()
+    if W.dtype.itemsize != 1 or W.numel() < n_blocks * BLOCK_BYTES:
+        raise ValueError("W must hold n_blocks * 136 bytes")
+    out = torch.empty(n_blocks * QK_K, dtype=torch.float32, device=W.device) if out is None else out
+    lib().check("dequant_iq4xs_gpu", W.data_ptr(), out.data_ptr(), n_blocks, 64, _stream(torch))
+    return out
 
 
 def synthetic_weights(K: int, N: int, seed: int, first_block: int = 0, device=None):

@@ -142,6 +142,12 @@ int gemm_iq4xs_stock_dp4a_gpu(const void* W, const float* X, float* Y, int64_t K
     return mul_mat_pooled(W, X, Y, K, N, M, LAYOUT_KM, as_stream(stream));
 }
 
+int dequant_iq4xs_gpu(const void* src, float* dst, int64_t n_blocks, int warp_size, void* stream) {
+    if (!src || !dst || n_blocks <= 0 || n_blocks >= MAX_DIM || (warp_size != 32 && warp_size != 64))
+        return hipErrorInvalidValue;
+    return launch_dequant(static_cast<const uint8_t*>(src), dst, n_blocks, as_stream(stream));
+}
+
 bool custom_gemv_iq4xs_can_handle(int64_t K, int64_t N, int64_t M, int type) {
     return type == IQ4XS_GGML_TYPE_IQ4_XS && M >= 1 && M <= GEMV_MAX_COLS && valid_k(K) && K < MAX_DIM && N > 0 &&
            N < MAX_DIM;

@@ -38,6 +38,9 @@ hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads,
 // C[32][32] = A B^T, through the operand layouts the GEMM uses.
 hipError_t launch_probe_mfma(const int8_t* A, const int8_t* B, int32_t* C, hipStream_t stream);
 
+// n_blocks super-blocks -> fp32 weights (256 per block, in block order).
+hipError_t launch_dequant(const uint8_t* src, float* dst, int64_t n_blocks, hipStream_t stream);
+
 hipError_t launch_fill_weights(uint8_t* W, int64_t n_blocks, uint64_t seed, int64_t first_block,
                                hipStream_t stream);
 hipError_t launch_fill_activations(float* x, int64_t n, uint64_t seed, int outliers, hipStream_t stream);

@@ -160,6 +160,33 @@ def test_q8_1_rounding_boundaries(pkg, orc, dev):
     assert np.array_equal(got, orc.quantize_q8_1_batched(X, K // 8, 8, LAYOUT_MK))
 
 
+# ------------------------------------------------------------------ dequantiser
+def test_dequant_bit_exact(pkg, orc, golden, dev):
+    """dequant_iq4xs_gpu == the reference's CPU dequantiser bit for bit: its
+    own outputs (golden fixtures from the compiled ref_cpu.cpp), the KAT
+    blocks' hand values, and the oracle on a large random matrix."""
+    import json, os
+    L = pkg.lib()
+    for name in ("gemv_512x48", "gemv_768x8_odd_superblocks", "gemm_256x8x5"):
+        W = golden[name + ".W"]
+        want = golden[name + ".dequant"].ravel()
+        got = pkg.dequant(D(W, dev), W.size // 136).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32)), name
+    with open(os.path.join(os.path.dirname(__file__), "golden", "iq4xs_kat_blocks.json")) as f:
+        kat = json.load(f)
+    for case in kat["cases"]:
+        W = np.frombuffer(bytes.fromhex(case["raw_hex"]), np.uint8).copy()
+        got = pkg.dequant(D(W, dev), case["n_blocks"]).cpu().numpy().reshape(case["n_blocks"], 256)
+        for blk, elem, value in case["hand_values"]:
+            assert got[int(blk), int(elem)] == np.float32(value), (case["name"], blk, elem)
+    K, N = 5120, 333
+    W = orc.gen_weights(K, N, seed=77)
+    got = pkg.dequant(D(W, dev), N * K // 256).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), orc.dequant(W, K, N).ravel().view(np.uint32))
+    y = torch.zeros(256, device=dev)
+    assert L.dequant_iq4xs_gpu(D(W, dev).data_ptr(), y.data_ptr(), 1, 48, stream()) == pkg.ERROR_INVALID_VALUE
+
+
 # ------------------------------------------------------------------ GEMV / GEMM kernels
 GEMV_CASES = [(256, 1, 1), (768, 7, 1), (1024, 64, 1), (5120, 333, 1), (4096, 4096, 1),
               (768, 9, 2), (1280, 65, 3), (2048, 130, 4), (256, 5, 5), (5120, 100, 6), (512, 77, 7),

@@ -385,3 +385,52 @@ def test_compute_metrics():
     m = compute_metrics(r, -r)
     assert m["cosine"] == pytest.approx(-1.0) and not m["pass"]
     assert compute_metrics(r, np.array([1, -2, np.nan], np.float32))["bad"]
+
+
+# ---------------------------------------------------------------- dequant mutation control
+def dequant_gate(ref, got):
+    """Acceptance gate of the reference's dequant harness
+    (kernels/demo_iq4xs_dequant/test_compare.cpp:76-111): max_abs < 1e-5,
+    mean_abs < 1e-6, cosine >= 0.99999, no NaN/Inf."""
+    ref = ref.astype(np.float64).ravel()
+    got = got.astype(np.float64).ravel()
+    diff = np.abs(ref - got)
+    denom = np.linalg.norm(ref) * np.linalg.norm(got)
+    cos = float(ref @ got / denom) if denom > 1e-12 else 1.0
+    return bool(np.isfinite(got).all() and diff.max() < 1e-5 and diff.mean() < 1e-6 and cos >= 0.99999)
+
+
+def np_dequant_fp32(W, K, N, mutate=None):
+    """fp32 dequant in the reference's operation order (dl = d*(ls-32) in fp32,
+    then dl*kv), optionally with the reference's planted bugs
+    (kernels/demo_iq4xs_dequant/impl_broken.hip:33-46): 'scale' builds ls with
+    hi << 3, 'swap' swaps the nibbles."""
+    B = W.view(BLOCK_IQ4_XS).reshape(N, K // 256)
+    qs = B["qs"].reshape(N, K // 256, 8, 16)
+    lo_n, hi_n = (qs >> 4, qs & 15) if mutate == "swap" else (qs & 15, qs >> 4)
+    vals = np.concatenate([KVALUES_IQ4NL[lo_n], KVALUES_IQ4NL[hi_n]], axis=3).astype(np.float32)
+    sl = B["scales_l"].astype(np.int64)
+    sh = B["scales_h"].astype(np.int64)
+    ib = np.arange(8)
+    shift = 3 if mutate == "scale" else 4
+    ls = ((sl[:, :, ib // 2] >> (4 * (ib & 1))) & 15) | (((sh[:, :, None] >> (2 * ib)) & 3) << shift)
+    d = B["d"].view(np.float16).astype(np.float32)
+    dl = (d[:, :, None] * (ls.astype(np.float32) - np.float32(32.0))).astype(np.float32)
+    return (dl[:, :, :, None] * vals).astype(np.float32).reshape(N, K)
+
+
+def test_dequant_mutation_control(orc, golden):
+    """The comparison discriminates: the oracle and the fp32 restatement
+    match the reference's own dequant outputs bit for bit, while each of the
+    reference's planted bugs, applied to the restatement, fails the
+    reference's gate (the mistakes are planted here on the CPU, never in a
+    GPU kernel)."""
+    for name in ("gemv_512x48", "gemm_256x8x5"):
+        W = golden[name + ".W"]
+        K, N = (int(v) for v in golden[name + ".shape"][:2])
+        ref = golden[name + ".dequant"].astype(np.float32).reshape(N, K)
+        assert np.array_equal(orc.dequant(W, K, N).view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(np_dequant_fp32(W, K, N).view(np.uint32), ref.view(np.uint32))
+        assert dequant_gate(ref, np_dequant_fp32(W, K, N))
+        for bug in ("scale", "swap"):
+            assert not dequant_gate(ref, np_dequant_fp32(W, K, N, mutate=bug)), (name, bug)
