@@ -86,7 +86,8 @@ int gemm_iq4xs_stock_dp4a_gpu(const void* W, const float* X, float* Y, int64_t K
 /* Replaces dequant_iq4xs_gpu, kernels/demo_iq4xs_dequant/impl.hip:51-69:
  * n_blocks super-blocks -> 256*n_blocks fp32 weights, bit-identical to the
  * reference's CPU dequantiser (ref_cpu.cpp:6-27).  warp_size is accepted for
- * signature compatibility (32 or 64); the kernel always runs wave64. */
+ * signature compatibility (32 or 64, anything else is hipErrorInvalidValue);
+ * the kernel always runs wave64.  n_blocks == 0 launches nothing and succeeds. */
 int dequant_iq4xs_gpu(const void* src, float* dst, int64_t n_blocks, int warp_size, void* stream);
 
 /* ============================ ggml mul_mat boundary ============================ */

@@ -143,8 +143,9 @@ int gemm_iq4xs_stock_dp4a_gpu(const void* W, const float* X, float* Y, int64_t K
 }
 
 int dequant_iq4xs_gpu(const void* src, float* dst, int64_t n_blocks, int warp_size, void* stream) {
-    if (!src || !dst || n_blocks <= 0 || n_blocks >= MAX_DIM || (warp_size != 32 && warp_size != 64))
-        return hipErrorInvalidValue;
+    if (n_blocks < 0 || n_blocks >= MAX_DIM || (warp_size != 32 && warp_size != 64)) return hipErrorInvalidValue;
+    if (n_blocks == 0) return hipSuccess;  // the reference launches a grid that writes nothing
+    if (!src || !dst) return hipErrorInvalidValue;
     return launch_dequant(static_cast<const uint8_t*>(src), dst, n_blocks, as_stream(stream));
 }
 
