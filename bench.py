@@ -20,8 +20,10 @@ dequant   IQ4_XS -> fp32 (dequant_iq4xs_gpu) over the seven weight matrices.
 extra     bs = 2, 4, 8 (the same GEMV-only measurement with 1 % x20
           outliers) and the int8-MFMA GEMM at M = 512 and 2048 (2*M*N*K over
           the average of back-to-back launches rotated over the layer copies).
-model_stream  64 distinct layers resident (12.30 GB): one bs=1 token (448
-          calls, graph) and one bs=512 pass (quantise + GEMM per call).
+producers iq4xs_rms_norm_q8_1 (K=5120, with residual) and iq4xs_swiglu_q8_1
+          (K=17408) at M = 1 and 512.
+model_stream  64 distinct layers resident (12.30 GB) run as a data chain
+          through the producers: one bs=1 token (graph) and one bs=512 pass.
 cpu_baseline  the reference's own FP64 oracle (kernels/matmul_iq4xs/ref_cpu.cpp,
           compiled into oracle/_ref) -- or this repository's restatement where
           that is absent -- on one host core, on a bounded sample.
@@ -142,12 +144,22 @@ def capture(torch, stream, fn, use_graph: bool):
 
 def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
     """`--model-layers` distinct layers of the seven projections resident at
-    once (64 layers = 12.30 GB).  bs=1: one token = every layer's seven calls
-    in order on one stream (each launch waits for the previous one, as a
-    layer-to-layer data chain would; the inputs stay fixed because chaining
-    the synthetic outputs would overflow the fp16 Q8_1 scale without the
-    model's normalisation layers).  bs=512: the same layers as M=512 GEMMs
-    (quantise + GEMM per call)."""
+    once (64 layers = 12.30 GB), run as a data chain: each layer's output feeds
+    the next layer's Q8_1 producer.  Per layer (row m of every tensor is one
+    token; bs=1 is M=1, prefill M=512):
+        h += down_prev; A = Q8_1(rmsnorm(h) * g_attn)       iq4xs_rms_norm_q8_1
+        q, k, v = W_q A, W_k A, W_v A                       iq4xs_mul_mat_q8_1
+        B = Q8_1(q)          (attention itself is outside this path: its
+                              output has q's shape and takes its place)
+        o = W_o B
+        h += o; A = Q8_1(rmsnorm(h) * g_ffn)
+        gate, up = W_gate A, W_up A
+        C = Q8_1(silu(gate) * up)                           iq4xs_swiglu_q8_1
+        down_prev = W_down C
+    The norm gains are 1/1145 so that the synthetic weights (rms ~16 per
+    element) keep every activation well inside the fp16 range of the Q8_1
+    scale.  Bandwidth is charged for the projections' bytes only; the time
+    includes the producers."""
     s = stream.cuda_stream
     dev = torch.device("cuda:0")
     weights = []
@@ -158,45 +170,68 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
             L.check("iq4xs_fill_synthetic_weights", W.data_ptr(), N * K // 256, 42, (1 << 40) + ((l * 7 + i) << 24), s)
             row.append(W)
         weights.append(row)
-    layer_bytes = sum(gemv_bytes(K, N) for _, K, N in SHAPES)
     total_w = sum(N * K // 256 * 136 for _, K, N in SHAPES) * args.model_layers
-    xs = [pkg.synthetic_activations(K, seed=700 + i, device=dev) for i, (_, K, _) in enumerate(SHAPES)]
-    ys = [torch.empty(N, device=dev) for (_, _, N) in SHAPES]
-    wss = [torch.empty(L.iq4xs_workspace_bytes(K, 1), dtype=torch.uint8, device=dev) for (_, K, _) in SHAPES]
-    torch.cuda.synchronize()
+    H_DIM, Q_DIM, FF_DIM = SHAPES[0][1], SHAPES[0][2], SHAPES[4][2]
+    gain = torch.full((H_DIM,), 1.0 / 1145.0, device=dev)
+    eps = 1e-6
+    P = pkg.PATH_AUTO
 
-    def token() -> None:
-        for l in range(args.model_layers):
-            for i, (_, K, N) in enumerate(SHAPES):
-                L.check("iq4xs_mul_mat", weights[l][i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), K, N, 1,
-                        pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
+    def chain(M: int):
+        h = pkg.synthetic_activations(M * H_DIM, seed=700, device=dev)
+        bufs = {name: torch.zeros((M, N), device=dev) for name, _, N in SHAPES}
+        wsA = torch.empty(L.iq4xs_workspace_bytes(H_DIM, M), dtype=torch.uint8, device=dev)
+        wsB = torch.empty(L.iq4xs_workspace_bytes(Q_DIM, M), dtype=torch.uint8, device=dev)
+        wsC = torch.empty(L.iq4xs_workspace_bytes(FF_DIM, M), dtype=torch.uint8, device=dev)
 
+        def mm(W, ws, name, K, N):
+            L.check("iq4xs_mul_mat_q8_1", W.data_ptr(), ws.data_ptr(), bufs[name].data_ptr(), K, N, M,
+                    pkg.LAYOUT_MK, P, s)
+
+        def run() -> None:
+            for l in range(args.model_layers):
+                Wl = weights[l]
+                L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["down_proj"].data_ptr(), h.data_ptr(),
+                        gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
+                for i in range(3):
+                    mm(Wl[i], wsA, *SHAPES[i])
+                L.check("iq4xs_quantize_q8_1", bufs["q_proj"].data_ptr(), Q_DIM, M, pkg.LAYOUT_MK, wsB.data_ptr(),
+                        wsB.numel(), s)
+                mm(Wl[3], wsB, *SHAPES[3])
+                L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["o_proj"].data_ptr(), h.data_ptr(),
+                        gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
+                mm(Wl[4], wsA, *SHAPES[4])
+                mm(Wl[5], wsA, *SHAPES[5])
+                L.check("iq4xs_swiglu_q8_1", bufs["gate_proj"].data_ptr(), bufs["up_proj"].data_ptr(), FF_DIM, M,
+                        wsC.data_ptr(), wsC.numel(), s)
+                mm(Wl[6], wsC, *SHAPES[6])
+
+        def finite() -> bool:
+            torch.cuda.synchronize()
+            return bool(torch.isfinite(h).all()) and all(bool(torch.isfinite(v).all()) for v in bufs.values())
+
+        return run, finite
+
+    layer_bytes = sum(gemv_bytes(K, N) for _, K, N in SHAPES)
+    token, finite1 = chain(1)
     run, launch = capture(torch, stream, token, use_graph)
     timer(run, 2)
     us = timer(run, 8) / 8
-    out = {"layers": args.model_layers, "weight_bytes": total_w,
-           "bs1": {"us_per_token": round(us, 1), "GBps": round(layer_bytes * args.model_layers / (us * 1e-6) / 1e9, 1),
-                   "frac_of_hbm_peak": round(layer_bytes * args.model_layers / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                   "tokens_per_s_upper_bound": round(1e6 / us, 1), "launch": launch}}
-    del run, xs, ys, wss
+    gbs = layer_bytes * args.model_layers / (us * 1e-6) / 1e9
+    out = {"layers": args.model_layers, "weight_bytes": total_w, "chain": "rmsnorm+residual -> q,k,v; q -> o; "
+           "rmsnorm+residual -> gate,up; swiglu -> down (producers write Q8_1)",
+           "bs1": {"us_per_token": round(us, 1), "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                   "tokens_per_s_upper_bound": round(1e6 / us, 1), "launch": launch, "finite": finite1()}}
+    del run
     M = 512
-    Xs = [pkg.synthetic_activations(K * M, seed=800 + i, device=dev) for i, (_, K, _) in enumerate(SHAPES)]
-    Ys = [torch.empty((M, N), device=dev) for (_, _, N) in SHAPES]
-    Ws = [torch.empty(L.iq4xs_workspace_bytes(K, M), dtype=torch.uint8, device=dev) for (_, K, _) in SHAPES]
-
-    def prefill() -> None:
-        for l in range(args.model_layers):
-            for i, (_, K, N) in enumerate(SHAPES):
-                L.check("iq4xs_mul_mat", weights[l][i].data_ptr(), Xs[i].data_ptr(), Ys[i].data_ptr(), K, N, M,
-                        pkg.LAYOUT_MK, Ws[i].data_ptr(), Ws[i].numel(), s)
-
+    prefill, finite512 = chain(M)
     prefill()
     torch.cuda.synchronize()
     us = timer(prefill, 1)
     ops = sum(2 * M * N * K for _, K, N in SHAPES) * args.model_layers
     out["bs512"] = {"ms_per_pass": round(us / 1e3, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
                     "frac_of_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
-                    "tokens_per_s": round(M / (us * 1e-6), 1), "includes": "Q8_1 quantisation of every call"}
+                    "tokens_per_s": round(M / (us * 1e-6), 1), "finite": finite512(),
+                    "includes": "the producers and the q re-quantisation of every layer"}
     return out
 
 
@@ -317,6 +352,41 @@ def main() -> int:
                "frac_of_hbm_peak": round(dq_bytes / (dq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                "bytes_per_superblock": "136 read + 1024 written", "shapes": "the seven projections of one layer"}
 
+    # ---- fused producers -> Q8_1 (decode M=1 and prefill M=512) ------------
+    producers = {}
+    H_DIM, FF_DIM, REPS = SHAPES[0][1], SHAPES[4][2], 32
+    for M in (1, 512):
+        X = pkg.synthetic_activations(M * H_DIM, seed=900, device=dev)
+        R = pkg.synthetic_activations(M * H_DIM, seed=901, device=dev)
+        Hh = torch.empty_like(X)
+        gn = torch.ones(H_DIM, device=dev)
+        G = pkg.synthetic_activations(M * FF_DIM, seed=902, device=dev)
+        U = pkg.synthetic_activations(M * FF_DIM, seed=903, device=dev)
+        wr = torch.empty(L.iq4xs_workspace_bytes(H_DIM, M), dtype=torch.uint8, device=dev)
+        wg = torch.empty(L.iq4xs_workspace_bytes(FF_DIM, M), dtype=torch.uint8, device=dev)
+
+        def rms_reps():
+            for _ in range(REPS):
+                L.check("iq4xs_rms_norm_q8_1", X.data_ptr(), R.data_ptr(), Hh.data_ptr(), gn.data_ptr(), 1e-6,
+                        H_DIM, M, wr.data_ptr(), wr.numel(), s)
+
+        def swiglu_reps():
+            for _ in range(REPS):
+                L.check("iq4xs_swiglu_q8_1", G.data_ptr(), U.data_ptr(), FF_DIM, M, wg.data_ptr(), wg.numel(), s)
+
+        row = {}
+        for name, fn, nbytes in (("rms_norm_q8_1", rms_reps, M * (H_DIM * 13 + H_DIM // 32 * 4)),
+                                 ("swiglu_q8_1", swiglu_reps, M * (FF_DIM * 9 + FF_DIM // 32 * 4))):
+            run_p, _ = capture(torch, stream, fn, use_graph)
+            us = timer(run_p, 4) / (4 * REPS)
+            row[name] = {"K": H_DIM if name == "rms_norm_q8_1" else FF_DIM, "us": round(us, 2),
+                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes}
+            del run_p
+        producers[str(M)] = row
+        del X, R, Hh, G, U, wr, wg
+    producers["bytes"] = ("rms: x, residual read + h written (4 B each), codes 1 B + ds 4 B per 32; "
+                          "swiglu: gate, up read (4 B each), codes + ds written")
+
     # ---- GEMM at M = 512 / 2048 on the same shapes -------------------------
     gemm = {}
     for M in args.gemm_m:
@@ -375,8 +445,10 @@ def main() -> int:
                      "kernel": "gemv_tile_kernel<1,2,false,false> (bs=1, prequantised Q8_1)",
                      "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps},
         "small_batch_gemv": small,
-        "gemm": {"peak_tops": INT8_PEAK_TOPS, "kernel": "gemm_iq4xs_mfma_kernel", "by_M": gemm},
+        "gemm": {"peak_tops": INT8_PEAK_TOPS, "by_M": gemm,
+                 "kernel": "gemm_iq4xs_db_kernel (128x128) or gemm_iq4xs_mfma_kernel (64x64), chosen per shape"},
         "dequant": dequant,
+        "producers": producers,
         "model_stream": model,
         "cpu_baseline": cpu,
         "host": platform.node(),

@@ -126,6 +126,28 @@ size_t iq4xs_workspace_bytes(int64_t K, int64_t M);
 int iq4xs_quantize_q8_1(const float* X, int64_t K, int64_t M, int layout, void* ws, size_t ws_bytes,
                         void* stream);
 
+/* Fused producers: the op that writes a mul_mat activation, quantised to
+ * planar Q8_1 in ws on the way out (row-major inputs, row m at [m*K]).  They
+ * stand for ggml's RMS_NORM + MUL and SWIGLU ahead of the projections
+ * (profiled by the reference at benchmarks/profiling/BOTTLENECK-TABLE.md:
+ * 24,26,30) and have no kernel counterpart in the reference; survey rank 2
+ * of the next steps.  K % 32 == 0.
+ *
+ * rms norm: h = X + R (R may be NULL), written to H when H is non-NULL
+ * (H may be exactly X or R: the in-place residual add); then
+ *   mean = (float)(sum (double)(h*h) / K), scale = 1.0f / sqrtf(mean + eps),
+ *   y = (h * scale) * gamma[k]       (gamma NULL: y = h * scale)
+ * with the sum in a fixed order, so results are reproducible bit for bit.
+ * The Qwen-27B-class models use eps = 1e-6
+ * (benchmarks/environment/startup-log.txt:128).  X, R, H 16-byte aligned. */
+int iq4xs_rms_norm_q8_1(const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                        int64_t M, void* ws, size_t ws_bytes, void* stream);
+
+/* swiglu: y = silu(G) * U, silu(g) = g / (1 + exp(-g)) (exp computed by the
+ * library's own Cody-Waite reduction, <= 1 ulp). */
+int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void* ws, size_t ws_bytes,
+                      void* stream);
+
 /* Y = W * dequant(ws) from an already quantised workspace; `layout` selects
  * the Y layout; `path` is one of IQ4XS_PATH_*. */
 int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,

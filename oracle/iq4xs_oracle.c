@@ -141,6 +141,117 @@ void orc_quantize_q8_1_batched(const float* X, orc_block_q8_1* Y, int64_t K, int
     }
 }
 
+/*
+ * ---------------------------------------------------------------------------
+ * Fused producers.  The reference's kernels stop at the quantiser; the op
+ * that writes the activation lives in ggml (RMS_NORM + MUL before the
+ * attention/FFN projections, SWIGLU before ffn_down; their cost is profiled
+ * in benchmarks/profiling/BOTTLENECK-TABLE.md:24,26,30, and the model's
+ * rms epsilon is 1e-6, benchmarks/environment/startup-log.txt:128).  The
+ * fp32 values below are this library's definition of those ops; they must
+ * be reproduced bit for bit by the device kernels, so every rounding step
+ * and the reduction order are spelled out.
+ * ---------------------------------------------------------------------------
+ */
+
+/*
+ * exp(x): Cody & Waite range reduction (x = n ln2 + r, ln2 split into a
+ * 16-significant-bit head, so n*head is exact for |n| <= 255, and a tail),
+ * then the degree-7 Taylor polynomial of e^r on |r| <= ln2/2 by Horner with
+ * fused multiply-adds (truncation error < 2^-27 relative), then r -> 2^n.
+ * Inputs below -87 are raised to -87 (no subnormal results: the only user
+ * adds the value to 1); above 88.72283935546875 the result is +inf.
+ */
+float orc_exp_cw(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e430p+6f) return INFINITY;
+    if (x < -87.0f) x = -87.0f;
+    const float n = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-n, 0x1.62e400p-1f, x);
+    r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+/* silu(x) = x / (1 + exp(-x)), the form ggml's SILU/SWIGLU use. */
+float orc_silu(float x) { return x / (1.0f + orc_exp_cw(-x)); }
+
+/* y = silu(g) * u, row-major [M][K]; y -> Q8_1 blocks [M][K/32]. */
+void orc_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, float* Y, orc_block_q8_1* out) {
+    const int64_t n = K * M;
+    for (int64_t i = 0; i < n; ++i) {
+        const float s = orc_silu(G[i]);
+        Y[i] = s * U[i];
+    }
+    orc_quantize_q8_1(Y, out, n);
+}
+
+/*
+ * RMS norm of one row h[K] (h = x + r when a residual r is given), then an
+ * elementwise gain, then Q8_1:
+ *   ss    = sum of (double)(h*h)            in the order below
+ *   mean  = (float)(ss / K)                 (division in double)
+ *   scale = 1.0f / sqrtf(mean + eps)
+ *   y     = (h * scale) * gamma             (two fp32 roundings; no gamma: h*scale)
+ * This is ggml's CPU rms_norm (double sum of float squares, float scale)
+ * followed by its MUL.  Summation order: element k goes to accumulator
+ * a = (k / 4) % 1024 (a work-group of 1024 threads reading 4-float vectors,
+ * 4096 elements per sweep), each accumulator adds its elements in increasing
+ * k; the 1024 accumulators reduce as sixteen 64-lane butterflies (v[l] +=
+ * v[l ^ o] for o = 32, 16, 8, 4, 2, 1, lane 0 kept) and then a pairwise tree
+ * over the 16 wave sums: ((w0 + w1) + (w2 + w3)) + ((w4 + w5) + (w6 + w7))
+ * and so on.
+ */
+static double rms_sum_squares(const float* h, int64_t K) {
+    enum { THREADS = 1024, WAVES = THREADS / 64 };
+    double acc[THREADS];
+    for (int a = 0; a < THREADS; ++a) acc[a] = 0.0;
+    for (int64_t k = 0; k < K; ++k) {
+        const float sq = h[k] * h[k];
+        acc[(k >> 2) & (THREADS - 1)] += (double)sq;
+    }
+    double w[WAVES];
+    for (int wv = 0; wv < WAVES; ++wv) {
+        double v[64];
+        for (int l = 0; l < 64; ++l) v[l] = acc[64 * wv + l];
+        for (int o = 32; o > 0; o >>= 1) {
+            double nv[64];
+            for (int l = 0; l < 64; ++l) nv[l] = v[l] + v[l ^ o];
+            memcpy(v, nv, sizeof nv);
+        }
+        w[wv] = v[0];
+    }
+    for (int n = WAVES / 2; n > 0; n >>= 1)
+        for (int i = 0; i < n; ++i) w[i] = w[2 * i] + w[2 * i + 1];
+    return w[0];
+}
+
+void orc_rms_norm_q8_1(const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                       int64_t M, float* Y, orc_block_q8_1* out) {
+    for (int64_t m = 0; m < M; ++m) {
+        const float* x = X + m * K;
+        float* y = Y + m * K;
+        /* h first lands in y (or H), so H may alias X or R */
+        float* h = H ? H + m * K : y;
+        for (int64_t k = 0; k < K; ++k) h[k] = R ? x[k] + R[m * K + k] : x[k];
+        const double ss = rms_sum_squares(h, K);
+        const float mean = (float)(ss / (double)K);
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (int64_t k = 0; k < K; ++k) {
+            const float t = h[k] * scale;
+            y[k] = gamma ? t * gamma[k] : t;
+        }
+        orc_quantize_q8_1(y, out + m * (K / ORC_QK8_1), K);
+    }
+}
+
 /* x_hat = fp16(d) * q : the values a Q8_1 path actually multiplies. */
 void orc_dequant_q8_1(const orc_block_q8_1* y, float* xhat, int64_t n_blocks) {
     for (int64_t b = 0; b < n_blocks; ++b) {

@@ -22,6 +22,14 @@
  *   orc_subblock_sums         exact int64 brute force over dequantised codes
  *   orc_gemv_fp64/gemm_fp64   bit-exact vs the compiled reference ref_cpu.cpp
  *                             golden outputs (tests/golden) and numpy float64
+ *   orc_exp_cw / orc_silu     error bound vs float64 exp / silu (<= 2 / 4 ulp)
+ *                             over a dense sweep, exact special values
+ *   orc_rms_norm_q8_1         scale vs float64 RMS within 2^-22 (eps-sensitive
+ *                             small-magnitude rows included), closed forms
+ *                             (constant rows, one nonzero), blocks through
+ *                             orc_quantize_q8_1 of the returned values
+ *   orc_swiglu_q8_1           values vs float64 silu(g)*u, blocks through
+ *                             orc_quantize_q8_1 of the returned values
  *   orc_gemv_semantics        fp32 summation ORDER of the gfx1100 kernel is
  *   orc_gemm_semantics        parity unpinned (no gfx1100 here); the integer
  *                             terms are pinned by orc_subblock_sums and the
@@ -84,6 +92,19 @@ void orc_gemv_fp64(const orc_block_iq4_xs* W, const float* x, float* y, int64_t 
 void orc_gemm_fp64(const orc_block_iq4_xs* W, const float* X, float* Y, int64_t K, int64_t N,
                    int64_t M, int nthreads);
 void orc_dequant(const orc_block_iq4_xs* W, float* out, int64_t K, int64_t N);
+
+/*
+ * Fused producers -> Q8_1 (no counterpart in the reference's kernels; they
+ * stand for the ggml ops that write a mul_mat activation).  The fp32 value
+ * each produces is defined exactly (reduction order included) so that the
+ * Q8_1 blocks it yields are bit-exact; the blocks themselves follow
+ * orc_quantize_q8_1.
+ */
+float orc_exp_cw(float x);
+float orc_silu(float x);
+void orc_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, float* Y, orc_block_q8_1* out);
+void orc_rms_norm_q8_1(const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                       int64_t M, float* Y, orc_block_q8_1* out);
 
 void orc_gen_weights(orc_block_iq4_xs* W, int64_t n_blocks, uint64_t seed, int64_t first_block);
 void orc_gen_activations(float* x, int64_t n, uint64_t seed, int outliers);

@@ -68,6 +68,10 @@ class Oracle:
             "orc_gemv_fp64": (None, [_P, _P, _P, _I64, _I64]),
             "orc_gemm_fp64": (None, [_P, _P, _P, _I64, _I64, _I64, ctypes.c_int]),
             "orc_dequant": (None, [_P, _P, _I64, _I64]),
+            "orc_exp_cw": (ctypes.c_float, [ctypes.c_float]),
+            "orc_silu": (ctypes.c_float, [ctypes.c_float]),
+            "orc_swiglu_q8_1": (None, [_P, _P, _I64, _I64, _P, _P]),
+            "orc_rms_norm_q8_1": (None, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, _P, _P]),
             "orc_gen_weights": (None, [_P, _I64, ctypes.c_uint64, _I64]),
             "orc_gen_activations": (None, [_P, _I64, ctypes.c_uint64, ctypes.c_int]),
         }
@@ -123,6 +127,38 @@ class Oracle:
         out = np.empty(nb * QK8_1, np.float32)
         self.lib.orc_dequant_q8_1(_ptr(np.ascontiguousarray(AQ)), _ptr(out), nb)
         return out
+
+    # --- fused producers -> Q8_1 ---------------------------------------
+    def exp_cw(self, x: np.ndarray) -> np.ndarray:
+        f = self.lib.orc_exp_cw
+        return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+
+    def silu(self, x: np.ndarray) -> np.ndarray:
+        f = self.lib.orc_silu
+        return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+
+    def swiglu_q8_1(self, G: np.ndarray, U: np.ndarray, K: int, M: int):
+        """(y [M][K] float32, Q8_1 blocks of y as bytes)."""
+        G = np.ascontiguousarray(G, dtype=np.float32)
+        U = np.ascontiguousarray(U, dtype=np.float32)
+        assert G.size == U.size == K * M
+        Y = np.empty((M, K), np.float32)
+        Q = np.zeros(M * (K // QK8_1) * Q8_1_BYTES, np.uint8)
+        self.lib.orc_swiglu_q8_1(_ptr(G), _ptr(U), K, M, _ptr(Y), _ptr(Q))
+        return Y, Q
+
+    def rms_norm_q8_1(self, X: np.ndarray, K: int, M: int, R=None, gamma=None, eps: float = 1e-6):
+        """(h = X + R [M][K], y [M][K], Q8_1 blocks of y as bytes)."""
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        assert X.size == K * M
+        H = np.empty((M, K), np.float32)
+        Y = np.empty((M, K), np.float32)
+        Q = np.zeros(M * (K // QK8_1) * Q8_1_BYTES, np.uint8)
+        Rp = None if R is None else np.ascontiguousarray(R, dtype=np.float32)
+        Gp = None if gamma is None else np.ascontiguousarray(gamma, dtype=np.float32)
+        self.lib.orc_rms_norm_q8_1(_ptr(X), None if Rp is None else _ptr(Rp), _ptr(H),
+                                   None if Gp is None else _ptr(Gp), eps, K, M, _ptr(Y), _ptr(Q))
+        return H, Y, Q
 
     # --- integer sums and outputs -------------------------------------
     def subblock_sums(self, W: np.ndarray, AQ: np.ndarray, K: int, N: int, M: int) -> np.ndarray:

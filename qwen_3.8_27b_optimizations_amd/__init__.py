@@ -58,6 +58,8 @@ SIGNATURES = {
     "iq4xs_mul_mat_q8_1": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _INT, _P]),
     "iq4xs_mul_mat": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, ctypes.c_size_t, _P]),
     "iq4xs_mul_mat_fused": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, _P]),
+    "iq4xs_rms_norm_q8_1": (_INT, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, _P, ctypes.c_size_t, _P]),
+    "iq4xs_swiglu_q8_1": (_INT, [_P, _P, _I64, _I64, _P, ctypes.c_size_t, _P]),
     "iq4xs_q8_1_to_blocks": (_INT, [_P, _P, _I64, _I64, _P]),
     "iq4xs_subblock_sums": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "iq4xs_probe_mfma_i8": (_INT, [_P, _P, _P, _P]),
@@ -137,6 +139,27 @@ def quantize_q8_1(X, K: int, M: int, layout: int = LAYOUT_MK, ws=None):
     torch = _torch()
     ws = workspace(K, M, X.device) if ws is None else ws
     lib().check("iq4xs_quantize_q8_1", X.data_ptr(), K, M, layout, ws.data_ptr(), ws.numel(), _stream(torch))
+    return ws
+
+
+def rms_norm_q8_1(X, K: int, M: int, residual=None, out_h=None, gamma=None, eps: float = 1e-6, ws=None):
+    """h = X (+ residual) -> planar Q8_1 of (h / rms(h)) * gamma.
+
+    out_h receives h when given (it may be X or residual itself: the in-place
+    residual add).  Returns the workspace."""
+    torch = _torch()
+    ws = workspace(K, M, X.device) if ws is None else ws
+    ptr = lambda t: None if t is None else t.data_ptr()
+    lib().check("iq4xs_rms_norm_q8_1", X.data_ptr(), ptr(residual), ptr(out_h), ptr(gamma), eps, K, M,
+                ws.data_ptr(), ws.numel(), _stream(torch))
+    return ws
+
+
+def swiglu_q8_1(G, U, K: int, M: int, ws=None):
+    """planar Q8_1 of silu(G) * U; returns the workspace."""
+    torch = _torch()
+    ws = workspace(K, M, G.device) if ws is None else ws
+    lib().check("iq4xs_swiglu_q8_1", G.data_ptr(), U.data_ptr(), K, M, ws.data_ptr(), ws.numel(), _stream(torch))
     return ws
 
 

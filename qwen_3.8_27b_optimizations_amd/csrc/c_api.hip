@@ -212,6 +212,40 @@ int iq4xs_mul_mat_fused(const void* W, const float* X, float* Y, int64_t K, int6
     return mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, S, as_stream(stream));
 }
 
+namespace {
+// [a, a + a_bytes) and [b, b + b_bytes) share a byte (null never overlaps).
+bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return a && b && x < y + b_bytes && y < x + a_bytes;
+}
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+}  // namespace
+
+int iq4xs_rms_norm_q8_1(const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                        int64_t M, void* ws, size_t ws_bytes, void* stream) {
+    if (!X || !ws || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
+    if (!(eps >= 0.0f) || ws_bytes < planar_bytes(K, M) || reinterpret_cast<uintptr_t>(ws) % 256 != 0)
+        return hipErrorInvalidValue;
+    if (!aligned16(X) || !aligned16(R) || !aligned16(H)) return hipErrorInvalidValue;
+    // H is either its own buffer or exactly X or R (an in-place residual add)
+    const size_t bytes = (size_t)K * (size_t)M * sizeof(float), wsb = planar_bytes(K, M);
+    if ((H != X && overlaps(H, bytes, X, bytes)) || (H != R && overlaps(H, bytes, R, bytes)))
+        return hipErrorInvalidValue;
+    if (overlaps(ws, wsb, X, bytes) || overlaps(ws, wsb, R, bytes) || overlaps(ws, wsb, H, bytes))
+        return hipErrorInvalidValue;
+    const Planar p = planar_view(ws, K, M);
+    return launch_rms_norm_q8_1(X, R, H, gamma, eps, K, M, p.qs, p.ds, as_stream(stream));
+}
+
+int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void* ws, size_t ws_bytes,
+                      void* stream) {
+    if (!G || !U || !ws || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM)
+        return hipErrorInvalidValue;
+    if (ws_bytes < planar_bytes(K, M) || reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
+    const Planar p = planar_view(ws, K, M);
+    return launch_swiglu_q8_1(G, U, K, M, p.qs, p.ds, as_stream(stream));
+}
+
 int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, void* stream) {
     if (!ws || !blocks || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
     const Planar p = planar_view(ws, K, M);

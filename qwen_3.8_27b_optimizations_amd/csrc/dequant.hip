@@ -50,6 +50,7 @@ __global__ __launch_bounds__(256) void dequant_iq4xs_kernel(const uint8_t* __res
 }
 
 hipError_t launch_dequant(const uint8_t* src, float* dst, int64_t n_blocks, hipStream_t stream) {
+    clear_launch_error();
     const int64_t threads = n_blocks * 16;
     const int64_t grid = (threads + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;

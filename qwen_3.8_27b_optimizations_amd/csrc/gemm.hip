@@ -314,6 +314,7 @@ static bool use_big_tiles(int64_t N, int64_t M) {
 
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    clear_launch_error();
     if (use_big_tiles(N, M)) {
         const int64_t gx = (N + G2_BN - 1) / G2_BN;
         const int64_t gy = (M + G2_BM - 1) / G2_BM;
@@ -360,6 +361,7 @@ __global__ __launch_bounds__(64) void probe_mfma_kernel(const int8_t* __restrict
 }
 
 hipError_t launch_probe_mfma(const int8_t* A, const int8_t* B, int32_t* C, hipStream_t stream) {
+    clear_launch_error();
     hipLaunchKernelGGL(probe_mfma_kernel, dim3(1), dim3(64), 0, stream, A, B, C);
     return hipGetLastError();
 }

@@ -847,11 +847,13 @@ static hipError_t dispatch_cols(const uint8_t* W, const int8_t* aqs, const uint3
 
 hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    clear_launch_error();
     return dispatch_cols(W, aqs, ads, nullptr, 0, 0, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
 }
 
 hipError_t launch_gemv_fused(const uint8_t* W, const float* X, int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N,
                              int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    clear_launch_error();
     return dispatch_cols(W, nullptr, nullptr, X, sc, sk, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
 }
 

@@ -5,6 +5,12 @@
 
 namespace iq4xs {
 
+// The runtime's last-error slot is per thread and shared with every other HIP
+// user in the process: a failure some earlier call left unread would be
+// reported as this library's.  Every launcher clears it first and then reads
+// its own launches' status with hipGetLastError.
+inline void clear_launch_error() { (void)hipGetLastError(); }
+
 // Activation / output layouts.
 constexpr int LAYOUT_KM = 0;  // X[k*M+m], Y[n*M+m]   (standalone API)
 constexpr int LAYOUT_MK = 1;  // X[m*K+k], Y[m*N+n]   (ggml src1 / dst)
@@ -40,6 +46,14 @@ hipError_t launch_probe_mfma(const int8_t* A, const int8_t* B, int32_t* C, hipSt
 
 // n_blocks super-blocks -> fp32 weights (256 per block, in block order).
 hipError_t launch_dequant(const uint8_t* src, float* dst, int64_t n_blocks, hipStream_t stream);
+
+// Producers writing the planar Q8_1 workspace (row-major [M][K] inputs).
+// rms norm: h = X (+ R) (stored to H when non-null; H may equal X or R),
+// y = (h * 1/sqrt(mean(h^2) + eps)) * gamma; swiglu: y = silu(G) * U.
+hipError_t launch_rms_norm_q8_1(const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                                int64_t M, int8_t* qs, uint32_t* ds, hipStream_t stream);
+hipError_t launch_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, int8_t* qs, uint32_t* ds,
+                              hipStream_t stream);
 
 hipError_t launch_fill_weights(uint8_t* W, int64_t n_blocks, uint64_t seed, int64_t first_block,
                                hipStream_t stream);

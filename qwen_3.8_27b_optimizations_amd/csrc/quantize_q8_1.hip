@@ -141,6 +141,7 @@ __global__ __launch_bounds__(256) void quantize_q8_1_rows_kernel(const float* __
 
 hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds,
                            block_q8_1* blocks, hipStream_t stream) {
+    clear_launch_error();
     const int64_t total = (K / QK8_1) * M;
     if (layout == LAYOUT_MK) {
         const int64_t grid = (total * 8 + 255) / 256;
@@ -158,6 +159,7 @@ hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int
 
 hipError_t launch_planar_to_blocks(const int8_t* qs, const uint32_t* ds, int64_t K, int64_t M, block_q8_1* blocks,
                                    hipStream_t stream) {
+    clear_launch_error();
     const int64_t total = (K / QK8_1) * M;
     const int64_t grid = (total + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;

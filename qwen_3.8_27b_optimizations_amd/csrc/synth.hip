@@ -71,6 +71,7 @@ __global__ __launch_bounds__(256) void fill_activations_kernel(float* __restrict
 }
 
 hipError_t launch_fill_weights(uint8_t* W, int64_t n_blocks, uint64_t seed, int64_t first_block, hipStream_t stream) {
+    clear_launch_error();
     const int64_t grid = (n_blocks + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(fill_weights_kernel, dim3((unsigned)grid), dim3(256), 0, stream, W, n_blocks, seed,
@@ -79,6 +80,7 @@ hipError_t launch_fill_weights(uint8_t* W, int64_t n_blocks, uint64_t seed, int6
 }
 
 hipError_t launch_fill_activations(float* x, int64_t n, uint64_t seed, int outliers, hipStream_t stream) {
+    clear_launch_error();
     const int64_t grid = (n + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(fill_activations_kernel, dim3((unsigned)grid), dim3(256), 0, stream, x, n, seed, outliers);
