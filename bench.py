@@ -176,7 +176,7 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
     eps = 1e-6
     P = pkg.PATH_AUTO
 
-    def chain(M: int):
+    def chain(M: int, grouped: bool = False):
         h = pkg.synthetic_activations(M * H_DIM, seed=700, device=dev)
         bufs = {name: torch.zeros((M, N), device=dev) for name, _, N in SHAPES}
         wsA = torch.empty(L.iq4xs_workspace_bytes(H_DIM, M), dtype=torch.uint8, device=dev)
@@ -187,20 +187,41 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
             L.check("iq4xs_mul_mat_q8_1", W.data_ptr(), ws.data_ptr(), bufs[name].data_ptr(), K, N, M,
                     pkg.LAYOUT_MK, P, s)
 
+        import ctypes
+
+        def group_args(Ws, names):
+            n = len(Ws)
+            return (n, (ctypes.c_void_p * n)(*[w.data_ptr() for w in Ws]),
+                    (ctypes.c_void_p * n)(*[bufs[nm].data_ptr() for nm in names]),
+                    (ctypes.c_int64 * n)(*[bufs[nm].shape[1] for nm in names]))
+
+        gargs = [(group_args(weights[l][0:3], ["q_proj", "k_proj", "v_proj"]),
+                  group_args(weights[l][4:6], ["gate_proj", "up_proj"])) for l in range(args.model_layers)]
+
+        def mm_group(l, which, ws, K):
+            n, wp, yp, nn = gargs[l][which]
+            L.check("iq4xs_mul_mat_q8_1_group", n, wp, yp, nn, ws.data_ptr(), K, M, pkg.LAYOUT_MK, s)
+
         def run() -> None:
             for l in range(args.model_layers):
                 Wl = weights[l]
                 L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["down_proj"].data_ptr(), h.data_ptr(),
                         gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
-                for i in range(3):
-                    mm(Wl[i], wsA, *SHAPES[i])
+                if grouped:
+                    mm_group(l, 0, wsA, H_DIM)
+                else:
+                    for i in range(3):
+                        mm(Wl[i], wsA, *SHAPES[i])
                 L.check("iq4xs_quantize_q8_1", bufs["q_proj"].data_ptr(), Q_DIM, M, pkg.LAYOUT_MK, wsB.data_ptr(),
                         wsB.numel(), s)
                 mm(Wl[3], wsB, *SHAPES[3])
                 L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["o_proj"].data_ptr(), h.data_ptr(),
                         gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
-                mm(Wl[4], wsA, *SHAPES[4])
-                mm(Wl[5], wsA, *SHAPES[5])
+                if grouped:
+                    mm_group(l, 1, wsA, H_DIM)
+                else:
+                    mm(Wl[4], wsA, *SHAPES[4])
+                    mm(Wl[5], wsA, *SHAPES[5])
                 L.check("iq4xs_swiglu_q8_1", bufs["gate_proj"].data_ptr(), bufs["up_proj"].data_ptr(), FF_DIM, M,
                         wsC.data_ptr(), wsC.numel(), s)
                 mm(Wl[6], wsC, *SHAPES[6])
@@ -221,6 +242,16 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
            "rmsnorm+residual -> gate,up; swiglu -> down (producers write Q8_1)",
            "bs1": {"us_per_token": round(us, 1), "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                    "tokens_per_s_upper_bound": round(1e6 / us, 1), "launch": launch, "finite": finite1()}}
+    del run
+    token_g, finite_g = chain(1, grouped=True)
+    run, _ = capture(torch, stream, token_g, use_graph)
+    timer(run, 2)
+    us = timer(run, 8) / 8
+    gbs = layer_bytes * args.model_layers / (us * 1e-6) / 1e9
+    out["bs1_grouped"] = {"us_per_token": round(us, 1), "GBps": round(gbs, 1),
+                          "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                          "tokens_per_s_upper_bound": round(1e6 / us, 1), "finite": finite_g(),
+                          "note": "same chain; q,k,v and gate,up each one iq4xs_mul_mat_q8_1_group launch"}
     del run
     M = 512
     prefill, finite512 = chain(M)
@@ -307,6 +338,36 @@ def main() -> int:
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    # ---- grouped decode set: q/k/v and gate/up as one launch each ----------
+    import ctypes
+
+    def group_args(Ws, Ys):
+        n = len(Ws)
+        return (n, (ctypes.c_void_p * n)(*[w.data_ptr() for w in Ws]), (ctypes.c_void_p * n)(*[y.data_ptr() for y in Ys]),
+                (ctypes.c_int64 * n)(*[y.numel() for y in Ys]))
+
+    groups = [(group_args(layers[l][0:3], ys[0:3]), group_args(layers[l][4:6], ys[4:6])) for l in range(args.layers)]
+
+    def grouped_rotation() -> None:
+        for l in range(args.layers):
+            (n, wp, yp, nn), (n2, wp2, yp2, nn2) = groups[l]
+            L.check("iq4xs_mul_mat_q8_1_group", n, wp, yp, nn, wss[0].data_ptr(), SHAPES[0][1], 1, pkg.LAYOUT_MK, s)
+            L.check("iq4xs_mul_mat_q8_1", layers[l][3].data_ptr(), wss[3].data_ptr(), ys[3].data_ptr(), SHAPES[3][1],
+                    SHAPES[3][2], 1, pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
+            L.check("iq4xs_mul_mat_q8_1_group", n2, wp2, yp2, nn2, wss[4].data_ptr(), SHAPES[4][1], 1, pkg.LAYOUT_MK, s)
+            L.check("iq4xs_mul_mat_q8_1", layers[l][6].data_ptr(), wss[6].data_ptr(), ys[6].data_ptr(), SHAPES[6][1],
+                    SHAPES[6][2], 1, pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
+
+    gr_run, _ = capture(torch, stream, grouped_rotation, use_graph)
+    timer(gr_run, 2)
+    gr_us = timer(gr_run, args.roofline_reps) / args.roofline_reps
+    gr_gbs = step_bytes * args.layers / (gr_us * 1e-6) / 1e9
+    grouped = {"GBps": round(gr_gbs, 1), "frac": round(gr_gbs / HBM_PEAK_GBS, 4),
+               "us_per_layer": round(gr_us / args.layers, 2), "launches_per_layer": 4,
+               "note": "iq4xs_mul_mat_q8_1_group: q,k,v in one launch, gate,up in one; o, down alone; "
+                       "prequantised Q8_1, same rotation and byte count as the roofline leg"}
+    del gr_run
 
     if args.copy_probe:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device=dev)
@@ -442,8 +503,9 @@ def main() -> int:
                    "launch": launch, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_tile_kernel<1,2,false,false> (bs=1, prequantised Q8_1)",
+                     "kernel": "gemv_tile_kernel<1,2,false,false,false> (bs=1, prequantised Q8_1)",
                      "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps},
+        "grouped_gemv": grouped,
         "small_batch_gemv": small,
         "gemm": {"peak_tops": INT8_PEAK_TOPS, "by_M": gemm,
                  "kernel": "gemm_iq4xs_db_kernel (128x128) or gemm_iq4xs_mfma_kernel (64x64), chosen per shape"},

@@ -153,6 +153,17 @@ int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void
 int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,
                        int path, void* stream);
 
+/* Several weight matrices (1 <= count <= 4, each N[i] x K) against the same
+ * quantised activations in ws: Y[i] = W[i] * dequant(ws), Y[i] laid out as
+ * `layout` selects.  For M <= 8 one GEMV launch covers every matrix (q/k/v,
+ * gate/up of a decode step), which pays the per-launch fixed cost once; each
+ * output is bit-identical to iq4xs_mul_mat_q8_1 on its own matrix.  M > 8
+ * runs the GEMM per matrix.  W, Y, N are host arrays of count entries.  No
+ * counterpart in the reference, which runs every projection as its own
+ * mul_mat. */
+int iq4xs_mul_mat_q8_1_group(int count, const void* const* W, float* const* Y, const int64_t* N, const void* ws,
+                             int64_t K, int64_t M, int layout, void* stream);
+
 /* Quantise + multiply in one call.  For M == 1 and K <= 6144 the quantisation
  * runs inside the GEMV kernel and ws is not written (it is still validated). */
 int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,

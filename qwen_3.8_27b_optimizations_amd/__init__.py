@@ -58,6 +58,7 @@ SIGNATURES = {
     "iq4xs_mul_mat_q8_1": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _INT, _P]),
     "iq4xs_mul_mat": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, ctypes.c_size_t, _P]),
     "iq4xs_mul_mat_fused": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, _P]),
+    "iq4xs_mul_mat_q8_1_group": (_INT, [_INT, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
     "iq4xs_rms_norm_q8_1": (_INT, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, _P, ctypes.c_size_t, _P]),
     "iq4xs_swiglu_q8_1": (_INT, [_P, _P, _I64, _I64, _P, ctypes.c_size_t, _P]),
     "iq4xs_q8_1_to_blocks": (_INT, [_P, _P, _I64, _I64, _P]),
@@ -180,6 +181,25 @@ def mul_mat_q8_1(W, ws, K: int, N: int, M: int, layout: int = LAYOUT_MK, path: i
     lib().check("iq4xs_mul_mat_q8_1", W.data_ptr(), ws.data_ptr(), out.data_ptr(), K, N, M, layout, path,
                 _stream(torch))
     return out
+
+
+def mul_mat_q8_1_group(Ws, ws, K: int, Ns, M: int, layout: int = LAYOUT_MK, outs=None):
+    """[W_i * dequant(ws)] for up to 4 matrices sharing the activations (one GEMV launch for M <= 8)."""
+    torch = _torch()
+    n = len(Ws)
+    if not 1 <= n <= 4 or len(Ns) != n:
+        raise ValueError("1 to 4 matrices, one N each")
+    for W, N in zip(Ws, Ns):
+        _check_weights(W, K, N)
+    if outs is None:
+        outs = [torch.empty((M, N) if layout == LAYOUT_MK else (N, M), dtype=torch.float32, device=Ws[0].device)
+                for N in Ns]
+    arr_p = ctypes.c_void_p * n
+    wp = arr_p(*[W.data_ptr() for W in Ws])
+    yp = arr_p(*[Y.data_ptr() for Y in outs])
+    nn = (ctypes.c_int64 * n)(*Ns)
+    lib().check("iq4xs_mul_mat_q8_1_group", n, wp, yp, nn, ws.data_ptr(), K, M, layout, _stream(torch))
+    return outs
 
 
 def mul_mat(W, X, K: int, N: int, M: int, layout: int = LAYOUT_MK, ws=None, out=None):

@@ -189,6 +189,27 @@ int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64
     return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, path, nullptr, as_stream(stream));
 }
 
+int iq4xs_mul_mat_q8_1_group(int count, const void* const* W, float* const* Y, const int64_t* N, const void* ws,
+                             int64_t K, int64_t M, int layout, void* stream) {
+    if (count < 1 || count > GEMV_GROUP_MAX || !W || !Y || !N) return hipErrorInvalidValue;
+    if (layout != LAYOUT_KM && layout != LAYOUT_MK) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
+    for (int i = 0; i < count; ++i)
+        if (!valid_mat(W[i], ws, Y[i], K, N[i], M)) return hipErrorInvalidValue;
+    if (M > GEMV_MAX_COLS) {  // the GEMM already fills the chip per matrix
+        for (int i = 0; i < count; ++i) {
+            const hipError_t e = mul_mat_planar(static_cast<const uint8_t*>(W[i]), ws, Y[i], K, N[i], M, layout,
+                                                IQ4XS_PATH_GEMM, nullptr, as_stream(stream));
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const Planar p = planar_view(ws, K, M);
+    const uint8_t* Wb[GEMV_GROUP_MAX];
+    for (int i = 0; i < count; ++i) Wb[i] = static_cast<const uint8_t*>(W[i]);
+    return launch_gemv_group(count, Wb, Y, N, p.qs, p.ds, K, M, layout == LAYOUT_MK, as_stream(stream));
+}
+
 int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
                   size_t ws_bytes, void* stream) {
     if (!valid_mat(W, X, Y, K, N, M) || !ws) return hipErrorInvalidValue;

@@ -531,12 +531,46 @@ __global__ __launch_bounds__(64 * FLAT_WAVES) void gemv_flat_kernel(
 // may cross steps and waves freely and the result is deterministic.
 constexpr int TILE_WAVES = 8;
 
-template <int C, int D, bool kDebug, bool kFuse>
+// Up to GEMV_GROUP_MAX weight matrices with the same K that read the same
+// activations, run by one launch: matrix g owns tiles [tile_end[g-1],
+// tile_end[g]).  Every output row is computed exactly as by a launch of its
+// own matrix (the tile size does not enter a row's arithmetic).
+struct GemvGroup {
+    const uint8_t* W[GEMV_GROUP_MAX];
+    float* Y[GEMV_GROUP_MAX];
+    int64_t ldy_m[GEMV_GROUP_MAX];
+    int N[GEMV_GROUP_MAX];
+    int tile_end[GEMV_GROUP_MAX];
+};
+
+template <int C, int D, bool kDebug, bool kFuse, bool kGroup>
 __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
-    const uint8_t* __restrict__ W, const int8_t* __restrict__ aqs, const uint32_t* __restrict__ ads,
-    const float* __restrict__ X, int64_t sc, int64_t sk, float* __restrict__ Y, int K, int N, int64_t ldy_m,
-    int64_t ldy_n, int rows_per_wg, int32_t* __restrict__ dbg) {
+    const GemvGroup grp, const int8_t* __restrict__ aqs, const uint32_t* __restrict__ ads,
+    const float* __restrict__ X, int64_t sc, int64_t sk, int K, int64_t ldy_n, int rows_per_wg,
+    int32_t* __restrict__ dbg) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const uint8_t* __restrict__ W = grp.W[0];
+    float* __restrict__ Y = grp.Y[0];
+    int64_t ldy_m = grp.ldy_m[0];
+    int N = grp.N[0], tile0 = 0;
+    if (kGroup) {
+        // this tile's matrix, by scalar selects (no dynamic index into the
+        // argument block); a single matrix skips this dependent argument
+        // read, which sits ahead of the first weight load
+        int g = 0;
+#pragma unroll
+        for (int i = 0; i + 1 < GEMV_GROUP_MAX; ++i) g += (int)blockIdx.x >= grp.tile_end[i] ? 1 : 0;
+#pragma unroll
+        for (int i = 1; i < GEMV_GROUP_MAX; ++i) {
+            if (g == i) {
+                W = grp.W[i];
+                Y = grp.Y[i];
+                ldy_m = grp.ldy_m[i];
+                N = grp.N[i];
+                tile0 = grp.tile_end[i - 1];
+            }
+        }
+    }
     const int bpr = K / QK_K, nb = K / QK8_1;
     int8_t* sq = reinterpret_cast<int8_t*>(lds);
     float* sdx = reinterpret_cast<float*>(lds + (size_t)C * K);
@@ -545,14 +579,14 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63, slot = lane >> 3, ib = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r0 = blockIdx.x * rows_per_wg;
+    const int r0 = ((int)blockIdx.x - tile0) * rows_per_wg;
     const int nrows = min(rows_per_wg, N - r0);
     const int n_sb = nrows * bpr;
     const int n_steps = (n_sb + 7) >> 3;
     const int my_n = wave < n_steps ? (n_steps - wave + TILE_WAVES - 1) / TILE_WAVES : 0;
     const uint8_t* Wg = W + (size_t)r0 * bpr * BLOCK_BYTES;
 
-    // Only the grid's last tile can end inside a step: there the lanes past
+    // Only a matrix's last tile can end inside a step: there the lanes past
     // the end re-read the last super-block and are not accumulated.
     const int last_step = n_steps - 1;
     const int last_slot = (n_sb - 1) - 8 * last_step;
@@ -646,11 +680,11 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     // Row sums: 16 lanes (one DPP row) per output row; lane g sums partials
     // g, g+16, ... in order, then a fixed DPP tree adds the 16 lanes.  Every
     // lane of a DPP row takes the same branches.
-    const int grp = tid >> 4, gl = tid & 15;
+    const int rgrp = tid >> 4, gl = tid & 15;
     const int n_grp = blockDim.x >> 4;
 #pragma unroll
     for (int cc = 0; cc < C; ++cc) {
-        for (int rl = grp; rl < nrows; rl += n_grp) {
+        for (int rl = rgrp; rl < nrows; rl += n_grp) {
             const float* pr = part + cc * rows_per_wg * bpr + rl * bpr;
             float v = 0.0f;
             for (int b = gl; b < bpr; b += 16) v += pr[b];
@@ -751,19 +785,41 @@ static int64_t tile_rows(int64_t bpr, int64_t N) {
     return ((units + tiles - 1) / tiles) * g;
 }
 
+// One launch over the matrices of `mats` (count >= 1, all with K columns);
+// hipErrorNotSupported when a tile's LDS does not fit.
+struct TileMat {
+    const uint8_t* W;
+    float* Y;
+    int64_t N, ldy_m;
+};
+
 template <int C, int D>
-static hipError_t launch_tile_d(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X,
-                                int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m, int64_t ldy_n,
-                                int32_t* dbg, int64_t R, hipStream_t stream) {
+static hipError_t launch_tile_d(const TileMat* mats, int count, const int8_t* aqs, const uint32_t* ads,
+                                const float* X, int64_t sc, int64_t sk, int64_t K, int64_t ldy_n, int32_t* dbg,
+                                int64_t R, hipStream_t stream) {
     const int64_t bpr = K / QK_K, nb = K / QK8_1;
-    const int64_t wgs = (N + R - 1) / R;
+    GemvGroup grp{};
+    int64_t wgs = 0;
+    for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
+        const TileMat& m = mats[i < count ? i : count - 1];
+        if (i < count) wgs += (m.N + R - 1) / R;
+        grp.W[i] = m.W;
+        grp.Y[i] = m.Y;
+        grp.ldy_m[i] = m.ldy_m;
+        grp.N[i] = (int)m.N;
+        grp.tile_end[i] = (int)(wgs < 0x7FFFFFFF ? wgs : 0x7FFFFFFF);
+    }
     const size_t lds = (size_t)C * K + (size_t)C * nb * 4 + (size_t)C * R * bpr * 4;
     if (lds > GEMV_LDS_BUDGET || wgs > 0x7FFFFFFF) return hipErrorNotSupported;
     const dim3 grid((unsigned)wgs), block(64 * TILE_WAVES);
 #define IQ4XS_LAUNCH_TILE(DBG, FUSE)                                                                              \
-    hipLaunchKernelGGL((gemv_tile_kernel<C, D, DBG, FUSE>), grid, block, lds, stream, W, aqs, ads, X, sc, sk, Y,  \
-                       (int)K, (int)N, ldy_m, ldy_n, (int)R, dbg)
-    if (X != nullptr) {
+    hipLaunchKernelGGL((gemv_tile_kernel<C, D, DBG, FUSE, false>), grid, block, lds, stream, grp, aqs, ads, X, sc, \
+                       sk, (int)K, ldy_n, (int)R, dbg)
+    if (count > 1) {
+        if (X != nullptr || dbg != nullptr) return hipErrorNotSupported;  // grouped: planar activations only
+        hipLaunchKernelGGL((gemv_tile_kernel<C, D, false, false, true>), grid, block, lds, stream, grp, aqs, ads, X,
+                           sc, sk, (int)K, ldy_n, (int)R, dbg);
+    } else if (X != nullptr) {
         if (dbg) IQ4XS_LAUNCH_TILE(true, true); else IQ4XS_LAUNCH_TILE(false, true);
     } else {
         if (dbg) IQ4XS_LAUNCH_TILE(true, false); else IQ4XS_LAUNCH_TILE(false, false);
@@ -773,16 +829,26 @@ static hipError_t launch_tile_d(const uint8_t* W, const int8_t* aqs, const uint3
 }
 
 template <int C>
+static hipError_t launch_tile_group(const TileMat* mats, int count, const int8_t* aqs, const uint32_t* ads,
+                                    const float* X, int64_t sc, int64_t sk, int64_t K, int64_t ldy_n, int32_t* dbg,
+                                    hipStream_t stream) {
+    const int64_t bpr = K / QK_K;
+    int64_t rows = 0;
+    for (int i = 0; i < count; ++i) rows += mats[i].N;
+    const int64_t R = tile_rows(bpr, rows);
+    if (R * bpr * BLOCK_BYTES >= ((int64_t)1 << 31) || rows >= ((int64_t)1 << 30)) return hipErrorNotSupported;
+    static const int depth = tuning_knob("IQ4XS_GEMV_TILE_D", 2, 2, 4);
+    if (depth == 3) return launch_tile_d<C, 3>(mats, count, aqs, ads, X, sc, sk, K, ldy_n, dbg, R, stream);
+    if (depth == 4) return launch_tile_d<C, 4>(mats, count, aqs, ads, X, sc, sk, K, ldy_n, dbg, R, stream);
+    return launch_tile_d<C, 2>(mats, count, aqs, ads, X, sc, sk, K, ldy_n, dbg, R, stream);
+}
+
+template <int C>
 static hipError_t launch_tile(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const float* X, int64_t sc,
                               int64_t sk, float* Y, int64_t K, int64_t N, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
                               hipStream_t stream) {
-    const int64_t bpr = K / QK_K;
-    const int64_t R = tile_rows(bpr, N);
-    if (R * bpr * BLOCK_BYTES >= ((int64_t)1 << 31)) return hipErrorNotSupported;
-    static const int depth = tuning_knob("IQ4XS_GEMV_TILE_D", 2, 2, 4);
-    if (depth == 3) return launch_tile_d<C, 3>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, R, stream);
-    if (depth == 4) return launch_tile_d<C, 4>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, R, stream);
-    return launch_tile_d<C, 2>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, R, stream);
+    const TileMat m{W, Y, N, ldy_m};
+    return launch_tile_group<C>(&m, 1, aqs, ads, X, sc, sk, K, ldy_n, dbg, stream);
 }
 
 template <int C>
@@ -843,6 +909,37 @@ static hipError_t dispatch_cols(const uint8_t* W, const int8_t* aqs, const uint3
         case 8: return launch_cols<8>(W, aqs, ads, X, sc, sk, Y, K, N, ldy_m, ldy_n, dbg, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
+                             const int8_t* aqs, const uint32_t* ads, int64_t K, int64_t M, bool layout_mk,
+                             hipStream_t stream) {
+    clear_launch_error();
+    TileMat mats[GEMV_GROUP_MAX];
+    for (int i = 0; i < count; ++i) mats[i] = {W[i], Y[i], N[i], layout_mk ? N[i] : 1};
+    const int64_t ldy_n = layout_mk ? 1 : M;
+    static const int kind = tuning_knob("IQ4XS_GEMV_KIND", 2, 0, 2);
+    hipError_t err = hipErrorNotSupported;
+    if (K / QK_K >= 8 && K <= (1 << 24) && kind == 2) {
+        switch (M) {
+            case 1: err = launch_tile_group<1>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 2: err = launch_tile_group<2>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 3: err = launch_tile_group<3>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 4: err = launch_tile_group<4>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 5: err = launch_tile_group<5>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 6: err = launch_tile_group<6>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 7: err = launch_tile_group<7>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 8: err = launch_tile_group<8>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            default: return hipErrorInvalidValue;
+        }
+        if (err != hipErrorNotSupported) return err;
+    }
+    // shapes the tile kernel does not take: one launch per matrix
+    for (int i = 0; i < count; ++i) {
+        err = dispatch_cols(W[i], aqs, ads, nullptr, 0, 0, Y[i], K, N[i], M, mats[i].ldy_m, ldy_n, nullptr, stream);
+        if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,

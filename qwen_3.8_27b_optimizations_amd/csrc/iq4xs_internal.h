@@ -30,6 +30,17 @@ hipError_t launch_planar_to_blocks(const int8_t* qs, const uint32_t* ds, int64_t
 hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
 
+// Matrices run together by one grouped GEMV launch (same K, same activations).
+constexpr int GEMV_GROUP_MAX = 4;
+
+// Y[i] = W[i] x for i < count <= GEMV_GROUP_MAX, M <= GEMV_MAX_COLS columns
+// of planar Q8_1 activations; Y[i] in ggml layout [M][N[i]] (layout_mk) or
+// [N[i]][M].  One launch when the tile kernel takes the shape, otherwise one
+// per matrix; outputs are bit-identical to launch_gemv on each matrix.
+hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
+                             const int8_t* aqs, const uint32_t* ads, int64_t K, int64_t M, bool layout_mk,
+                             hipStream_t stream);
+
 // Same contract with fp32 activations quantised inside the kernel (element
 // (m, k) at X[m*sc + k*sk]); hipErrorNotSupported if the shape does not fit
 // the fused kernel's LDS budget (then quantise separately).
