@@ -9,6 +9,14 @@
 // gemm_iq4xs_db_kernel (128x128 tile, 16 waves, double-buffered LDS) and
 // gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves, four per CU).
 //
+// Both are VALU-issue bound: the fp32 scaling costs 3 VALU ops per output and
+// sub-block (convert, scale product, fused add) against 1/16 of a 32x32x32
+// int8 MFMA.  Measured on the 128x128 kernel: removing the int8 MFMA changes
+// little, every VALU op removed shows up in full, forming the scale product
+// with an f32 MFMA (32x32x2, a rank-1 outer product) costs as much as the 16
+// multiplies it replaces, and keeping (ls - 32) as int8 with d_w applied once
+// per super-block (exact int32 sumi*(ls-32)) is 4-8 % slower.
+//
 // MI355X mapping (64x64 kernel).  A workgroup (4 waves) owns a 64-row x
 // 64-token output tile and walks K one 256-weight super-block at a time:
 //   1. the 64 weight rows' super-blocks are decoded (v_perm codebook lookup,
