@@ -863,6 +863,17 @@ static hipError_t launch_flat_depth(const uint8_t* W, const int8_t* aqs, const u
     }
 }
 
+// Planar columns that go to the matrix-core GEMV: its cost per weight byte
+// does not grow with the columns, the dot4 kernels' does.  Measured per
+// projection shape (K 5120-17408): it wins from 6 columns on when N >= 2048;
+// below that, and for narrow matrices (k/v, N = 1024: too few 32-row blocks
+// to fill the chip), the dot4 kernels are faster.  Grouped launches use the
+// same rule per matrix, so their outputs match single calls bit for bit.
+static bool use_gemv_mfma(int64_t N, int64_t M) {
+    static const int min_cols = tuning_knob("IQ4XS_GEMV_MFMA_MIN_COLS", 6, 1, 9);
+    return M >= min_cols && N >= 2048;
+}
+
 // X == nullptr: planar Q8_1 activations (aqs, ads); otherwise fp32 X quantised
 // in the prologue (fused; returns hipErrorNotSupported when it does not fit).
 template <int C>
@@ -871,6 +882,10 @@ static hipError_t launch_cols(const uint8_t* W, const int8_t* aqs, const uint32_
                               hipStream_t stream) {
     const int64_t bpr = K / QK_K;
     hipError_t err = hipErrorNotSupported;
+    if (X == nullptr && use_gemv_mfma(N, C)) {
+        err = launch_gemv_mfma(W, aqs, ads, Y, K, N, C, ldy_m, ldy_n, dbg, stream);
+        if (err != hipErrorNotSupported) return err;
+    }
     static const int kind = tuning_knob("IQ4XS_GEMV_KIND", 2, 0, 2);  // 0 items, 1 flat, 2 tile
     const bool fits = K <= (1 << 24) && N < (1 << 30);
     if (fits && bpr >= 8 && kind == 2)
@@ -920,7 +935,9 @@ hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y
     const int64_t ldy_n = layout_mk ? 1 : M;
     static const int kind = tuning_knob("IQ4XS_GEMV_KIND", 2, 0, 2);
     hipError_t err = hipErrorNotSupported;
-    if (K / QK_K >= 8 && K <= (1 << 24) && kind == 2) {
+    bool any_mfma = false;
+    for (int i = 0; i < count; ++i) any_mfma = any_mfma || use_gemv_mfma(N[i], M);
+    if (K / QK_K >= 8 && K <= (1 << 24) && kind == 2 && !any_mfma) {
         switch (M) {
             case 1: err = launch_tile_group<1>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
             case 2: err = launch_tile_group<2>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;

@@ -1,0 +1,168 @@
+// gemv_mfma.hip -- small-batch IQ4_XS x Q8_1 GEMV (2 <= M <= 8 columns) on
+// the gfx950 int8 matrix cores.
+//
+// Semantics: those of the GEMV / GEMM (real_stock_dp4a_comparator.hip:
+// 68-166, 374-443): per 32-weight sub-block the exact int32 dot sumi of the
+// IQ4_XS codes with the Q8_1 codes, scaled by fp16(d_w)*(ls-32) and the
+// column's fp16 d.
+//
+// Why a second GEMV.  The dot4 GEMV spends VALU work per weight byte and per
+// column, so from 4 columns on it is VALU-bound (bs = 8 ran at 1.35 TB/s).
+// Here one v_mfma_i32_32x32x32_i8 takes 32 weight rows x 32 k of one
+// sub-block against all columns at once (the A operand is the activations,
+// one token per MFMA row; rows past M hold any token and only produce C rows
+// that are never stored), so the VALU cost per weight byte no longer grows
+// with M: decoding the codes into the B operand, then per useful output a
+// convert, a scale product and a fused add.
+//
+// Mapping.  A workgroup of GM_WAVES waves owns 32 weight rows; its waves take
+// the super-blocks kb = wave, wave + GM_WAVES, ... (at any moment they stream
+// GM_WAVES consecutive super-blocks of the same rows), each wave keeping one
+// super-block of loads in flight while it computes the previous one.  The
+// MFMA sums over k, so any order of k that A and B share gives the same
+// int32: lane l (half h = l >> 5) supplies weight row l & 31 with both
+// nibbles of qs bytes 8h .. 8h+7 of the sub-block (sub-block weights
+// 8h .. 8h+7 and 16+8h .. 16+8h+7), decoded in registers, and the A lanes the
+// activation codes of the same 16 weights.  The C element e of lane l is
+// token 8*(e>>2) + 4h + (e&3) of that row.  Token scales are staged in LDS
+// once ([sub-block][8]), and each wave stages its super-block's activations
+// (M x 256 codes, two 16-byte loads per lane) in LDS rows of its own before
+// reading its MFMA A operands from them.  The GM_WAVES partial sums of every
+// output are added in LDS in wave order (deterministic).
+#include "iq4xs_device.h"
+#include "iq4xs_internal.h"
+
+namespace iq4xs {
+
+constexpr int GM_WAVES = 8;
+
+constexpr int GM_AROW = 272;  // LDS row of one token's 256 codes, padded (bank spread)
+
+struct GmPref {
+    v2u h;       // d, scales_h, scales_l of the super-block
+    v2u q[8];    // qs bytes 8h .. 8h+7 of each sub-block
+    v4i a[2];    // 32 of the super-block's activation codes: token lane/8, bytes 32*(lane%8) ..
+};
+
+template <bool kDebug>
+__global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t* __restrict__ W,
+                                                                  const int8_t* __restrict__ aqs,
+                                                                  const uint32_t* __restrict__ ads,
+                                                                  float* __restrict__ Y, int K, int N, int M,
+                                                                  int64_t ldy_m, int64_t ldy_n,
+                                                                  int32_t* __restrict__ dbg) {
+    constexpr int G = 1;  // M <= 8: tokens 4h + e of element e < 4
+    extern __shared__ __attribute__((aligned(16))) float gm_lds[];
+    const int bpr = K / QK_K, nb = K / QK8_1;
+    float* sdx = gm_lds;                        // [nb][8G] column scales, 0 past M
+    float* red = gm_lds + (size_t)nb * 8 * G;   // [GM_WAVES][4G][64] partial sums
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, col = lane & 31;
+    int8_t* sact = reinterpret_cast<int8_t*>(red + GM_WAVES * 4 * G * 64) + (tid >> 6) * 8 * GM_AROW;  // [8][272]
+    const int wave = tid >> 6;
+    const int r0 = blockIdx.x * 32;
+    const int row = min(r0 + col, N - 1);     // rows past N computed, never stored
+    const uint8_t* wrow = W + (size_t)row * bpr * BLOCK_BYTES;
+    // this lane's share of a super-block's activations, and its MFMA A row in LDS
+    const int8_t* aload = aqs + (size_t)min(lane >> 3, M - 1) * K + 32 * (lane & 7);
+    int8_t* awrite = sact + (lane >> 3) * GM_AROW + 32 * (lane & 7);
+    const int8_t* aread = sact + min(col, M - 1) * GM_AROW + 8 * h;
+
+    for (int i = tid; i < nb * 8 * G; i += 64 * GM_WAVES) {
+        const int s = i / (8 * G), t = i - s * 8 * G;
+        sdx[i] = t < M ? half_bits_to_float(ads[(size_t)t * nb + s] & 0xFFFFu) : 0.0f;
+    }
+
+    const int my_n = wave < bpr ? (bpr - wave + GM_WAVES - 1) / GM_WAVES : 0;
+    auto load = [&](GmPref& p, int kb) {
+        const uint8_t* blk = wrow + (size_t)kb * BLOCK_BYTES;
+        p.h = *reinterpret_cast<const v2u*>(blk);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) p.q[s] = *reinterpret_cast<const v2u*>(blk + 8 + 16 * s + 8 * h);
+        p.a[0] = *reinterpret_cast<const v4i*>(aload + (size_t)kb * QK_K);
+        p.a[1] = *reinterpret_cast<const v4i*>(aload + (size_t)kb * QK_K + 16);
+    };
+
+    float acc[4 * G];
+#pragma unroll
+    for (int e = 0; e < 4 * G; ++e) acc[e] = 0.0f;
+    auto compute = [&](const GmPref& p, int kb) {
+        // the wave's own LDS rows: written here, read below by other lanes of
+        // the same wave (LDS operations of one wave complete in order; the
+        // previous super-block's reads were issued before these writes)
+        *reinterpret_cast<v4i*>(awrite) = p.a[0];
+        *reinterpret_cast<v4i*>(awrite + 16) = p.a[1];
+        const float dw = half_bits_to_float(p.h.x & 0xFFFFu);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            uint32_t lo0, hi0, lo1, hi1;
+            decode_codes_x(p.q[s].x, lo0, hi0);
+            decode_codes_x(p.q[s].y, lo1, hi1);
+            const v4i b = v4i{(int)lo0, (int)lo1, (int)hi0, (int)hi1};
+            const v2u a0 = *reinterpret_cast<const v2u*>(aread + 32 * s);
+            const v2u a1 = *reinterpret_cast<const v2u*>(aread + 32 * s + 16);
+            const v4i a = v4i{(int)a0.x, (int)a0.y, (int)a1.x, (int)a1.y};
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
+            const int ls = subblock_ls(p.h.x, p.h.y, s) - 32;
+            const float sa = dw * (float)ls;
+            const float* bxp = sdx + (kb * 8 + s) * 8 * G + 4 * h;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const v4f bx = *reinterpret_cast<const v4f*>(bxp + 8 * g);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * g + j;
+                    acc[e] = __builtin_fmaf((float)c[e], sa * bx[j], acc[e]);
+                    if (kDebug) {
+                        const int t = 8 * g + 4 * h + j;
+                        if (t < M && r0 + col < N) dbg[((size_t)t * N + r0 + col) * nb + kb * 8 + s] = c[e] * ls;
+                    }
+                }
+            }
+        }
+    };
+    // ring of 2 with constant indices (unrolled by its depth); every load is
+    // unconditional (past this wave's last super-block it repeats that one)
+    GmPref buf[2];
+    if (my_n > 0) load(buf[0], wave);
+    __syncthreads();  // column scales staged
+    for (int i0 = 0; i0 < my_n; i0 += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const int i = i0 + d;
+            load(buf[d ^ 1], wave + GM_WAVES * min(i + 1, my_n - 1));
+            if (i < my_n) compute(buf[d], wave + GM_WAVES * i);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4 * G; ++e) red[(wave * 4 * G + e) * 64 + lane] = acc[e];
+    __syncthreads();
+    if (wave == 0 && r0 + col < N) {
+#pragma unroll
+        for (int e = 0; e < 4 * G; ++e) {
+            float v = red[e * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < GM_WAVES; ++w) v += red[(w * 4 * G + e) * 64 + lane];
+            const int t = 8 * (e >> 2) + 4 * h + (e & 3);
+            if (t < M) Y[t * ldy_m + (int64_t)(r0 + col) * ldy_n] = v;
+        }
+    }
+}
+
+hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K,
+                            int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    clear_launch_error();
+    if (M < 1 || M > 8 || K % QK_K || K >= (1 << 24) || N >= (1 << 30)) return hipErrorNotSupported;
+    const size_t lds = ((size_t)(K / QK8_1) * 8 + (size_t)GM_WAVES * 4 * 64) * sizeof(float) +
+                       (size_t)GM_WAVES * 8 * GM_AROW;
+    if (lds > 64 * 1024) return hipErrorNotSupported;
+    const dim3 grid((unsigned)((N + 31) / 32)), block(64 * GM_WAVES);
+    if (dbg)
+        hipLaunchKernelGGL((gemv_mfma_kernel<true>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N, (int)M,
+                           ldy_m, ldy_n, dbg);
+    else
+        hipLaunchKernelGGL((gemv_mfma_kernel<false>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N,
+                           (int)M, ldy_m, ldy_n, dbg);
+    return hipGetLastError();
+}
+
+}  // namespace iq4xs

@@ -30,6 +30,11 @@ hipError_t launch_planar_to_blocks(const int8_t* qs, const uint32_t* ds, int64_t
 hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
 
+// Small-batch GEMV on the int8 matrix cores (1 <= M <= 8, same contract as
+// launch_gemv); hipErrorNotSupported when the shape does not fit its LDS.
+hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K,
+                            int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
+
 // Matrices run together by one grouped GEMV launch (same K, same activations).
 constexpr int GEMV_GROUP_MAX = 4;
 

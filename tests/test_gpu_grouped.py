@@ -23,7 +23,8 @@ GROUP_CASES = [  # K, Ns, M, layout
     (5120, (8192, 1024, 1024), 1, LAYOUT_MK),     # q, k, v of a decode step
     (5120, (17408, 17408), 1, LAYOUT_MK),         # gate, up
     (2048, (7, 130, 1, 64), 3, LAYOUT_KM),        # ragged last tiles, N = 1
-    (17408, (5120, 96), 8, LAYOUT_MK),
+    (17408, (5120, 96), 8, LAYOUT_MK),            # matrix-core GEMV for the wide one, dot4 for the other
+    (5120, (8192, 1024, 1024), 6, LAYOUT_KM),
     (8192, (5120,), 2, LAYOUT_KM),
     (1024, (40, 33, 9), 2, LAYOUT_MK),            # K < 2048: one launch per matrix
     (2048, (300, 64), 20, LAYOUT_MK),             # M > 8: the GEMM per matrix

@@ -197,7 +197,10 @@ def test_dequant_bit_exact(pkg, orc, golden, dev):
 # ------------------------------------------------------------------ GEMV / GEMM kernels
 GEMV_CASES = [(256, 1, 1), (768, 7, 1), (1024, 64, 1), (5120, 333, 1), (4096, 4096, 1),
               (768, 9, 2), (1280, 65, 3), (2048, 130, 4), (256, 5, 5), (5120, 100, 6), (512, 77, 7),
-              (8192, 96, 8), (17408, 40, 8)]
+              (8192, 96, 8), (17408, 40, 8),
+              # N >= 2048 and M >= 6: the matrix-core GEMV (ragged last 32-row block; fewer
+              # super-blocks than waves; long K)
+              (2048, 2048 + 33, 6), (768, 2051, 7), (5120, 2048, 8), (17408, 2080, 7)]
 
 
 @pytest.mark.parametrize("K,N,M", GEMV_CASES)
@@ -222,8 +225,11 @@ FUSED_CASES = [(256, 1, 1, LAYOUT_MK), (5120, 333, 1, LAYOUT_MK), (17408, 40, 1,
 
 @pytest.mark.parametrize("K,N,M,layout", FUSED_CASES)
 def test_fused_quantize_gemv(pkg, orc, dev, K, N, M, layout):
-    """One-launch path (Q8_1 quantisation in the GEMV prologue) == the
-    two-launch path bit for bit: same codes, same d, same summation order."""
+    """One-launch path (Q8_1 quantisation in the GEMV prologue) against the
+    two-launch path: the same codes, d and int32 sub-block sums always; for a
+    single column the same kernel, hence bit-identical outputs; for several
+    columns the two-launch path runs the matrix-core GEMV, whose fp32
+    summation order differs (held to the path's tolerance instead)."""
     W = orc.gen_weights(K, N, seed=5000 + K + N)
     X = orc.gen_activations(K * M, seed=6000 + M, outliers=True).reshape(M, K)
     if M == 1 and K == 5120:
@@ -236,7 +242,11 @@ def test_fused_quantize_gemv(pkg, orc, dev, K, N, M, layout):
     Yp = pkg.mul_mat_q8_1(Wd, ws, K, N, M, layout, pkg.PATH_GEMV)
     torch.cuda.synchronize()
     assert np.array_equal(Sf.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, M))
-    assert torch.equal(Yf, Yp)
+    if M == 1:
+        assert torch.equal(Yf, Yp)
+    else:
+        m = compute_metrics(Yp.cpu().numpy(), Yf.cpu().numpy())
+        assert m["rel_l2"] <= REL_L2_TOL and not m["bad"], m
     Ymn = Yf.cpu().numpy() if layout == LAYOUT_MK else Yf.cpu().numpy().T
     check_outputs(orc, W, AQ, Ymn, K, N, M, "fused")
 
