@@ -15,36 +15,39 @@
 // with M: decoding the codes into the B operand, then per useful output a
 // convert, a scale product and a fused add.
 //
-// Mapping.  A workgroup of GM_WAVES waves owns 32 weight rows; its waves take
+// Mapping.  A workgroup of GM_WAVES (8 or 16) waves owns 32 weight rows; its waves take
 // the super-blocks kb = wave, wave + GM_WAVES, ... (at any moment they stream
 // GM_WAVES consecutive super-blocks of the same rows), each wave keeping one
-// super-block of loads in flight while it computes the previous one.  The
+// super-block of loads in flight while it computes the previous one.  Its
+// loads are coalesced (each of the 4 weight loads covers the qs of 8 whole
+// rows, the 2 activation loads a token's 256 codes per 8 lanes) and staged in
+// LDS rows of the wave's own, from which the MFMA operands are read.  The
 // MFMA sums over k, so any order of k that A and B share gives the same
 // int32: lane l (half h = l >> 5) supplies weight row l & 31 with both
 // nibbles of qs bytes 8h .. 8h+7 of the sub-block (sub-block weights
 // 8h .. 8h+7 and 16+8h .. 16+8h+7), decoded in registers, and the A lanes the
 // activation codes of the same 16 weights.  The C element e of lane l is
 // token 8*(e>>2) + 4h + (e&3) of that row.  Token scales are staged in LDS
-// once ([sub-block][8]), and each wave stages its super-block's activations
-// (M x 256 codes, two 16-byte loads per lane) in LDS rows of its own before
-// reading its MFMA A operands from them.  The GM_WAVES partial sums of every
-// output are added in LDS in wave order (deterministic).
+// once ([sub-block][8]).  The GM_WAVES partial sums of every output are
+// added in LDS in wave order (deterministic).
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 
 namespace iq4xs {
 
-constexpr int GM_WAVES = 8;
+constexpr int GM_LDS_MAX = 160 * 1024;
 
 constexpr int GM_AROW = 272;  // LDS row of one token's 256 codes, padded (bank spread)
+constexpr int GM_WROW = 144;  // LDS row of one weight row's 128 qs bytes, padded
+constexpr int GM_WAVE_LDS = 32 * GM_WROW + 8 * GM_AROW;  // per-wave staging bytes
 
 struct GmPref {
-    v2u h;       // d, scales_h, scales_l of the super-block
-    v2u q[8];    // qs bytes 8h .. 8h+7 of each sub-block
+    v2u h;       // d, scales_h, scales_l of this lane's row's super-block
+    v4i q[4];    // qs chunk (lane % 8) of rows lane/8 + 8i: 8 whole rows per load instruction
     v4i a[2];    // 32 of the super-block's activation codes: token lane/8, bytes 32*(lane%8) ..
 };
 
-template <bool kDebug>
+template <int GM_WAVES, bool kDebug>
 __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t* __restrict__ W,
                                                                   const int8_t* __restrict__ aqs,
                                                                   const uint32_t* __restrict__ ads,
@@ -57,11 +60,19 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     float* sdx = gm_lds;                        // [nb][8G] column scales, 0 past M
     float* red = gm_lds + (size_t)nb * 8 * G;   // [GM_WAVES][4G][64] partial sums
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, col = lane & 31;
-    int8_t* sact = reinterpret_cast<int8_t*>(red + GM_WAVES * 4 * G * 64) + (tid >> 6) * 8 * GM_AROW;  // [8][272]
+    uint8_t* swave = reinterpret_cast<uint8_t*>(red + GM_WAVES * 4 * G * 64) + (tid >> 6) * GM_WAVE_LDS;
+    uint8_t* sw = swave;                                          // [32][144] qs of the 32 rows
+    int8_t* sact = reinterpret_cast<int8_t*>(swave + 32 * GM_WROW);  // [8][272] activations
     const int wave = tid >> 6;
     const int r0 = blockIdx.x * 32;
     const int row = min(r0 + col, N - 1);     // rows past N computed, never stored
-    const uint8_t* wrow = W + (size_t)row * bpr * BLOCK_BYTES;
+    const uint8_t* wrow = W + (size_t)row * bpr * BLOCK_BYTES;   // this lane's row (header)
+    const uint8_t* wchunk[4];                                      // rows lane/8 + 8i, qs chunk lane%8
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        wchunk[i] = W + (size_t)min(r0 + (lane >> 3) + 8 * i, N - 1) * bpr * BLOCK_BYTES + 8 + 16 * (lane & 7);
+    uint8_t* wwrite = sw + (lane >> 3) * GM_WROW + 16 * (lane & 7);
+    const uint8_t* wread = sw + col * GM_WROW + 8 * h;
     // this lane's share of a super-block's activations, and its MFMA A row in LDS
     const int8_t* aload = aqs + (size_t)min(lane >> 3, M - 1) * K + 32 * (lane & 7);
     int8_t* awrite = sact + (lane >> 3) * GM_AROW + 32 * (lane & 7);
@@ -74,10 +85,9 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
 
     const int my_n = wave < bpr ? (bpr - wave + GM_WAVES - 1) / GM_WAVES : 0;
     auto load = [&](GmPref& p, int kb) {
-        const uint8_t* blk = wrow + (size_t)kb * BLOCK_BYTES;
-        p.h = *reinterpret_cast<const v2u*>(blk);
+        p.h = *reinterpret_cast<const v2u*>(wrow + (size_t)kb * BLOCK_BYTES);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) p.q[s] = *reinterpret_cast<const v2u*>(blk + 8 + 16 * s + 8 * h);
+        for (int i = 0; i < 4; ++i) p.q[i] = *reinterpret_cast<const v4i_a8*>(wchunk[i] + (size_t)kb * BLOCK_BYTES);
         p.a[0] = *reinterpret_cast<const v4i*>(aload + (size_t)kb * QK_K);
         p.a[1] = *reinterpret_cast<const v4i*>(aload + (size_t)kb * QK_K + 16);
     };
@@ -91,12 +101,15 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
         // previous super-block's reads were issued before these writes)
         *reinterpret_cast<v4i*>(awrite) = p.a[0];
         *reinterpret_cast<v4i*>(awrite + 16) = p.a[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(wwrite + 8 * i * GM_WROW) = p.q[i];
         const float dw = half_bits_to_float(p.h.x & 0xFFFFu);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             uint32_t lo0, hi0, lo1, hi1;
-            decode_codes_x(p.q[s].x, lo0, hi0);
-            decode_codes_x(p.q[s].y, lo1, hi1);
+            const v2u q = *reinterpret_cast<const v2u*>(wread + 16 * s);
+            decode_codes_x(q.x, lo0, hi0);
+            decode_codes_x(q.y, lo1, hi1);
             const v4i b = v4i{(int)lo0, (int)lo1, (int)hi0, (int)hi1};
             const v2u a0 = *reinterpret_cast<const v2u*>(aread + 32 * s);
             const v2u a1 = *reinterpret_cast<const v2u*>(aread + 32 * s + 16);
@@ -148,21 +161,52 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     }
 }
 
+template <int WAVES>
+static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
+                            int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    const size_t lds = ((size_t)(K / QK8_1) * 8 + (size_t)WAVES * 4 * 64) * sizeof(float) +
+                       (size_t)WAVES * GM_WAVE_LDS;
+    if (lds > GM_LDS_MAX) return hipErrorNotSupported;
+    if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit of a launch
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_mfma_kernel<WAVES, false>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS_MAX);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_mfma_kernel<WAVES, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS_MAX);
+        if (e != hipSuccess) return e;
+    }
+    const dim3 grid((unsigned)((N + 31) / 32)), block(64 * WAVES);
+    if (dbg)
+        hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, true>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N,
+                           (int)M, ldy_m, ldy_n, dbg);
+    else
+        hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, false>), grid, block, lds, stream, W, aqs, ads, Y, (int)K,
+                           (int)N, (int)M, ldy_m, ldy_n, dbg);
+    return hipGetLastError();
+}
+
+static int gm_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K,
                             int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     clear_launch_error();
     if (M < 1 || M > 8 || K % QK_K || K >= (1 << 24) || N >= (1 << 30)) return hipErrorNotSupported;
-    const size_t lds = ((size_t)(K / QK8_1) * 8 + (size_t)GM_WAVES * 4 * 64) * sizeof(float) +
-                       (size_t)GM_WAVES * 8 * GM_AROW;
-    if (lds > 64 * 1024) return hipErrorNotSupported;
-    const dim3 grid((unsigned)((N + 31) / 32)), block(64 * GM_WAVES);
-    if (dbg)
-        hipLaunchKernelGGL((gemv_mfma_kernel<true>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N, (int)M,
-                           ldy_m, ldy_n, dbg);
-    else
-        hipLaunchKernelGGL((gemv_mfma_kernel<false>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N,
-                           (int)M, ldy_m, ldy_n, dbg);
-    return hipGetLastError();
+    // Parallelism comes from splitting K over the waves of a 32-row block:
+    // with fewer blocks than two per CU, 16 waves each (measured: q, o and
+    // down 5-15 % faster), otherwise 8 (gate/up: 16 would leave fewer
+    // workgroups resident per CU).
+    if ((N + 31) / 32 < 2 * gm_cu_count()) return launch_gm<16>(W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
+    return launch_gm<8>(W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
 }
 
 }  // namespace iq4xs
