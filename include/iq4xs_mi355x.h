@@ -77,6 +77,58 @@ int gemv_iq4xs_stock_dp4a_gpu(const void* W, const float* x, float* y, int64_t K
  * (same contract as gemv_iq4xs_stock_dp4a_gpu). */
 int gemv_iq4xs_dp4a_coop_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
 
+/* Replaces gemv_iq4xs_dp4a_gfx1100_gpu, impl_gemv_dp4a_gfx1100.hip:310-329
+ * (same contract as gemv_iq4xs_stock_dp4a_gpu). */
+int gemv_iq4xs_dp4a_gfx1100_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
+
+/* Replaces gemv_iq4xs_dp4a_gfx1100_prequantized_gpu, impl_gemv_dp4a_gfx1100.hip:291-308:
+ * y = W * dequant(AQ) for activations already quantised into the reference's
+ * 64-byte padded Q8_1 blocks (ds at byte 0, the 32 codes at bytes 16..47;
+ * impl_gemv_dp4a_gfx1100.hip:60-66), K/32 of them, 16-byte aligned.  The
+ * blocks are copied to a planar workspace from the stream-ordered pool. */
+int gemv_iq4xs_dp4a_gfx1100_prequantized_gpu(const void* W, const void* AQ, float* y, int64_t K, int64_t N,
+                                             void* stream);
+
+/* Replaces the FP64 comparators gemv_iq4xs_stock_gpu / gemm_iq4xs_stock_gpu,
+ * stock_hip_comparator.hip:120-151 (X [K][M], Y [N][M]): per output one double
+ * sum of (double)(fp16 d * (ls-32)) * kvalue * (double)x in the loop order of
+ * ref_cpu.cpp:12-106, products and sums rounded separately, so the outputs
+ * equal the reference's CPU FP64 oracle bit for bit.  One thread per output:
+ * a comparator, not a fast path. */
+int gemv_iq4xs_stock_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
+int gemm_iq4xs_stock_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, void* stream);
+
+/* Replaces gemv_iq4xs_gfx1100_gpu, impl_gemv_gfx1100.hip:99-120: the same FP64
+ * products, summed as 8 partials per row (one per sub-block index, over all
+ * super-blocks) that are then added in index order, as that kernel does. */
+int gemv_iq4xs_gfx1100_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
+
+/* Replace the fp16-WMMA GEMM family and its tiled fallbacks:
+ * gemm_iq4xs_wmma_stream_gpu / _wmma_p4_xor_gpu / _wmma_64x64_gpu and
+ * gemm_iq4xs_stream_tiled_gpu (impl_gemm_wmma_stream.hip:321-364),
+ * gemm_iq4xs_wmma_gpu / gemm_iq4xs_tiled_gpu (impl_gemm_wmma.hip:199-242).
+ * Same signature and layout as gemm_iq4xs_stock_dp4a_gpu (X [K][M], Y [N][M]),
+ * same argument checks.  They run this library's int8 GEMM on Q8_1 activations:
+ * the reference's fp16 numerics (dequantised weights x fp16-cast activations)
+ * are not reproduced. */
+int gemm_iq4xs_wmma_stream_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                               void* stream);
+int gemm_iq4xs_wmma_p4_xor_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                               void* stream);
+int gemm_iq4xs_wmma_64x64_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                              void* stream);
+int gemm_iq4xs_stream_tiled_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                                void* stream);
+int gemm_iq4xs_wmma_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, void* stream);
+int gemm_iq4xs_tiled_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, void* stream);
+
+/* Replaces gemm_iq4xs_lut_gpu, impl_gemm_lut_iq4xs.hip:138-157.  The codebook
+ * table LUT is accepted and not read (IQ4_XS fixes it).  Same gate as the
+ * reference: hipErrorInvalidConfiguration unless M, N, K are multiples of 16
+ * with M >= 512, N >= 32, K >= 32; otherwise as gemm_iq4xs_stock_dp4a_gpu. */
+int gemm_iq4xs_lut_gpu(const void* W, const void* LUT, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                       void* stream);
+
 /* Replaces gemm_iq4xs_stock_dp4a_gpu, real_stock_dp4a_comparator.hip:505-548:
  * Y[n*M + m] = sum_k W[n,k] X[k*M + m].  M <= 8 runs the streaming GEMV,
  * larger M the int8-MFMA GEMM. */

@@ -404,6 +404,37 @@ void orc_gemm_fp64(const orc_block_iq4_xs* W, const float* X, float* Y, int64_t 
 }
 
 /* kernels/matmul_iq4xs/ref_cpu.cpp:108-139 -- fp32 dequantisation. */
+/*
+ * impl_gemv_gfx1100.hip:6-93 -- the FP64 GEMV of the
+ * reference's gfx1100 kernel: the products of ref_cpu.cpp, summed as 8
+ * partials per row (partial ib runs over all super-blocks b, j = 0..15, low
+ * then high nibble), the partials then added in ib order.
+ */
+void orc_gemv_fp64_by_subblock(const orc_block_iq4_xs* W, const float* x, float* y, int64_t K, int64_t N) {
+    const int64_t bpr = K / ORC_QK_K;
+    for (int64_t r = 0; r < N; ++r) {
+        double part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int ib = 0; ib < 8; ++ib) {
+            for (int64_t b = 0; b < bpr; ++b) {
+                const orc_block_iq4_xs* blk = W + r * bpr + b;
+                const float d = orc_fp16_to_fp32(blk->d);
+                const double dl = (double)d * (double)((float)orc_subblock_scale(blk, ib) - 32.0f);
+                const float* xs = x + b * ORC_QK_K + ib * 32;
+                for (int j = 0; j < 16; ++j) {
+                    const uint8_t q = blk->qs[ib * 16 + j];
+                    const double wl = dl * (double)orc_kvalues_iq4nl[q & 15];
+                    const double wh = dl * (double)orc_kvalues_iq4nl[q >> 4];
+                    part[ib] += wl * (double)xs[j];
+                    part[ib] += wh * (double)xs[j + 16];
+                }
+            }
+        }
+        double acc = 0.0;
+        for (int ib = 0; ib < 8; ++ib) acc += part[ib];
+        y[r] = (float)acc;
+    }
+}
+
 void orc_dequant(const orc_block_iq4_xs* W, float* out, int64_t K, int64_t N) {
     const int64_t bpr = K / ORC_QK_K;
     for (int64_t r = 0; r < N; ++r)

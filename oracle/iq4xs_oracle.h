@@ -22,6 +22,8 @@
  *   orc_subblock_sums         exact int64 brute force over dequantised codes
  *   orc_gemv_fp64/gemm_fp64   bit-exact vs the compiled reference ref_cpu.cpp
  *                             golden outputs (tests/golden) and numpy float64
+ *   orc_gemv_fp64_by_subblock numpy float64 (1e-12), and the golden FP64
+ *                             outputs to float rounding
  *   orc_exp_cw / orc_silu     error bound vs float64 exp / silu (<= 2 / 4 ulp)
  *                             over a dense sweep, exact special values
  *   orc_rms_norm_q8_1         scale vs float64 RMS within 2^-22 (eps-sensitive
@@ -92,6 +94,7 @@ void orc_gemv_fp64(const orc_block_iq4_xs* W, const float* x, float* y, int64_t 
 void orc_gemm_fp64(const orc_block_iq4_xs* W, const float* X, float* Y, int64_t K, int64_t N,
                    int64_t M, int nthreads);
 void orc_dequant(const orc_block_iq4_xs* W, float* out, int64_t K, int64_t N);
+void orc_gemv_fp64_by_subblock(const orc_block_iq4_xs* W, const float* x, float* y, int64_t K, int64_t N);
 
 /*
  * Fused producers -> Q8_1 (no counterpart in the reference's kernels; they

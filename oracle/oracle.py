@@ -68,6 +68,7 @@ class Oracle:
             "orc_gemv_fp64": (None, [_P, _P, _P, _I64, _I64]),
             "orc_gemm_fp64": (None, [_P, _P, _P, _I64, _I64, _I64, ctypes.c_int]),
             "orc_dequant": (None, [_P, _P, _I64, _I64]),
+            "orc_gemv_fp64_by_subblock": (None, [_P, _P, _P, _I64, _I64]),
             "orc_exp_cw": (ctypes.c_float, [ctypes.c_float]),
             "orc_silu": (ctypes.c_float, [ctypes.c_float]),
             "orc_swiglu_q8_1": (None, [_P, _P, _I64, _I64, _P, _P]),
@@ -189,6 +190,12 @@ class Oracle:
         Y = np.empty((N, M), np.float32)
         self.lib.orc_gemm_fp64(_ptr(W), _ptr(X_km), _ptr(Y), K, N, M, nthreads)
         return Y
+
+    def gemv_fp64_by_subblock(self, W: np.ndarray, x: np.ndarray, K: int, N: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(N, np.float32)
+        self.lib.orc_gemv_fp64_by_subblock(_ptr(W), _ptr(x), _ptr(y), K, N)
+        return y
 
     def dequant(self, W: np.ndarray, K: int, N: int) -> np.ndarray:
         out = np.empty((N, K), np.float32)

@@ -49,6 +49,18 @@ SIGNATURES = {
     "gemv_iq4xs_dp4a_coop_gpu": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "gemm_iq4xs_stock_dp4a_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "dequant_iq4xs_gpu": (_INT, [_P, _P, _I64, _INT, _P]),
+    "gemv_iq4xs_dp4a_gfx1100_gpu": (_INT, [_P, _P, _P, _I64, _I64, _P]),
+    "gemv_iq4xs_dp4a_gfx1100_prequantized_gpu": (_INT, [_P, _P, _P, _I64, _I64, _P]),
+    "gemv_iq4xs_stock_gpu": (_INT, [_P, _P, _P, _I64, _I64, _P]),
+    "gemm_iq4xs_stock_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "gemv_iq4xs_gfx1100_gpu": (_INT, [_P, _P, _P, _I64, _I64, _P]),
+    "gemm_iq4xs_wmma_stream_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "gemm_iq4xs_wmma_p4_xor_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "gemm_iq4xs_wmma_64x64_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "gemm_iq4xs_stream_tiled_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "gemm_iq4xs_wmma_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "gemm_iq4xs_tiled_gpu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "gemm_iq4xs_lut_gpu": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "custom_gemv_iq4xs_can_handle": (ctypes.c_bool, [_I64, _I64, _I64, _INT]),
     "custom_gemv_iq4xs_dispatch": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "custom_gemm_iq4xs_can_handle": (ctypes.c_bool, [_I64, _I64, _I64, _INT]),

@@ -63,6 +63,14 @@ hipError_t launch_probe_mfma(const int8_t* A, const int8_t* B, int32_t* C, hipSt
 // n_blocks super-blocks -> fp32 weights (256 per block, in block order).
 hipError_t launch_dequant(const uint8_t* src, float* dst, int64_t n_blocks, hipStream_t stream);
 
+// FP64 comparators in the reference's loop orders (stock: X [K][M] -> Y [N][M];
+// gfx1100: one column) and the 64-byte padded Q8_1 blocks of its cooperative
+// GEMV -> planar workspace (one column of nb blocks).
+hipError_t launch_stock_fp64(const uint8_t* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                             hipStream_t stream);
+hipError_t launch_gfx1100_fp64(const uint8_t* W, const float* x, float* y, int64_t K, int64_t N, hipStream_t stream);
+hipError_t launch_coop_to_planar(const uint8_t* coop, int64_t nb, int8_t* qs, uint32_t* ds, hipStream_t stream);
+
 // Producers writing the planar Q8_1 workspace (row-major [M][K] inputs).
 // rms norm: h = X (+ R) (stored to H when non-null; H may equal X or R),
 // y = (h * 1/sqrt(mean(h^2) + eps)) * gamma; swiglu: y = silu(G) * U.

@@ -99,6 +99,18 @@ def test_invalid_arguments_rejected_before_launch(L, pkg):
     assert L.iq4xs_probe_mfma_i8(None, FAKE, FAKE, None) == E
     assert L.iq4xs_fill_synthetic_weights(FAKE, 0, 1, 0, None) == E
     assert L.iq4xs_fill_synthetic_activations(None, 10, 1, 0, None) == E
+    assert L.gemv_iq4xs_dp4a_gfx1100_gpu(FAKE, FAKE, None, 256, 4, None) == E
+    assert L.gemv_iq4xs_dp4a_gfx1100_prequantized_gpu(FAKE, None, FAKE, 256, 4, None) == E
+    assert L.gemv_iq4xs_dp4a_gfx1100_prequantized_gpu(FAKE, ctypes.c_void_p(0x100008), FAKE, 256, 4, None) == E
+    assert L.gemv_iq4xs_stock_gpu(FAKE, FAKE, FAKE, 100, 4, None) == E
+    assert L.gemv_iq4xs_gfx1100_gpu(FAKE, FAKE, FAKE, 256, 0, None) == E
+    assert L.gemm_iq4xs_stock_gpu(FAKE, FAKE, FAKE, 256, 4, 0, None) == E
+    for name in ("gemm_iq4xs_wmma_stream_gpu", "gemm_iq4xs_wmma_p4_xor_gpu", "gemm_iq4xs_wmma_64x64_gpu",
+                 "gemm_iq4xs_stream_tiled_gpu", "gemm_iq4xs_wmma_gpu", "gemm_iq4xs_tiled_gpu"):
+        assert getattr(L, name)(FAKE, FAKE, FAKE, 300, 4, 4, None) == E, name
+    assert L.gemm_iq4xs_lut_gpu(FAKE, FAKE, None, FAKE, 256, 64, 512, None) == E
+    # the reference's LUT shape gate: refused before any launch
+    assert L.gemm_iq4xs_lut_gpu(FAKE, FAKE, FAKE, FAKE, 256, 64, 256, None) == pkg.ERROR_INVALID_CONFIG
 
 
 def test_product_package_has_no_oracle_dependency():

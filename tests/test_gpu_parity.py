@@ -183,12 +183,12 @@ def test_dequant_bit_exact(pkg, orc, golden, dev):
     W = orc.gen_weights(K, N, seed=77)
     got = pkg.dequant(D(W, dev), N * K // 256).cpu().numpy()
     assert np.array_equal(got.view(np.uint32), orc.dequant(W, K, N).ravel().view(np.uint32))
-    y = torch.zeros(256, device=dev)
-    assert L.dequant_iq4xs_gpu(D(W, dev).data_ptr(), y.data_ptr(), 1, 48, stream()) == pkg.ERROR_INVALID_VALUE
+    Wd, y = D(W, dev), torch.zeros(256, device=dev)
+    assert L.dequant_iq4xs_gpu(Wd.data_ptr(), y.data_ptr(), 1, 48, stream()) == pkg.ERROR_INVALID_VALUE
     # warp_size 32 selects the same kernel; an empty matrix writes nothing
     got32 = torch.full((256,), -1.0, device=dev)
-    assert L.dequant_iq4xs_gpu(D(W, dev).data_ptr(), got32.data_ptr(), 1, 32, stream()) == 0
-    assert L.dequant_iq4xs_gpu(D(W, dev).data_ptr(), y.data_ptr(), 0, 64, stream()) == 0
+    assert L.dequant_iq4xs_gpu(Wd.data_ptr(), got32.data_ptr(), 1, 32, stream()) == 0
+    assert L.dequant_iq4xs_gpu(Wd.data_ptr(), y.data_ptr(), 0, 64, stream()) == 0
     torch.cuda.synchronize()
     assert np.array_equal(got32.cpu().numpy().view(np.uint32), orc.dequant(W, K, N).ravel()[:256].view(np.uint32))
     assert not y.any()

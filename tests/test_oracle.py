@@ -434,3 +434,37 @@ def test_dequant_mutation_control(orc, golden):
         assert dequant_gate(ref, np_dequant_fp32(W, K, N))
         for bug in ("scale", "swap"):
             assert not dequant_gate(ref, np_dequant_fp32(W, K, N, mutate=bug)), (name, bug)
+
+
+def test_fp64_by_subblock_order(orc, golden):
+    """The gfx1100 FP64 order (8 per-sub-block partials, then added) holds the
+    same products as ref_cpu.cpp in another order: against the reference's
+    own FP64 outputs it may differ by the final float rounding only, and
+    against numpy float64 it is exact to 1e-12."""
+    for name in ("gemv_512x48", "gemv_768x8_odd_superblocks", "gemv_1024x16_outliers"):
+        W, x, y_ref = golden[name + ".W"], golden[name + ".x"], golden[name + ".y"].astype(np.float32)
+        K, N = (int(v) for v in golden[name + ".shape"][:2])
+        y = orc.gemv_fp64_by_subblock(W, x, K, N)
+        ulp = np.abs(y.astype(np.float64) - y_ref.astype(np.float64)) / np.spacing(np.abs(y_ref)).astype(np.float64)
+        assert ulp.max() <= 1.0, (name, ulp.max())
+        y64 = np_dequant64(W, K, N) @ x.astype(np.float64)
+        assert np.allclose(y, y64, rtol=1e-6, atol=1e-6)
+
+
+def test_fp64_by_subblock_order_is_distinguishable(orc):
+    """A cancellation that only the per-sub-block order survives: every weight
+    is exactly 1 (d = 1.0, ls = 33, code 8 -> +1), and x holds +2^80 at
+    (super-block 0, sub-block 0), 1 at (0, 1) and -2^80 at (1, 0).  The
+    sequential order of ref_cpu.cpp adds 1 to 2^80 (lost) and ends at 0; the
+    gfx1100 order cancels sub-block 0's partial first and ends at 1."""
+    K, N = 512, 2
+    blk = np.zeros(136, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:4] = (0xAA, 0xAA)          # hi bits 2 for every sub-block
+    blk[4:8] = 0x11                  # lo bits 1 for every sub-block -> ls = 33
+    blk[8:] = 0x88                   # both nibbles code 8 -> kvalue +1
+    W = np.tile(blk, K // 256 * N)
+    x = np.zeros(K, np.float32)
+    x[0], x[32], x[256] = 2.0 ** 80, 1.0, -(2.0 ** 80)
+    assert np.array_equal(orc.gemv_fp64(W, x, K, N), np.zeros(N, np.float32))
+    assert np.array_equal(orc.gemv_fp64_by_subblock(W, x, K, N), np.ones(N, np.float32))
