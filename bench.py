@@ -26,7 +26,9 @@ model_stream  64 distinct layers resident (12.30 GB) run as a data chain
           through the producers: one bs=1 token (graph) and one bs=512 pass.
 cpu_baseline  the reference's own FP64 oracle (kernels/matmul_iq4xs/ref_cpu.cpp,
           compiled into oracle/_ref) -- or this repository's restatement where
-          that is absent -- on one host core, on a bounded sample.
+          that is absent -- on one host core, on a bounded sample; beside it
+          (int8_host) the integer path on the host's cores (Q8_1 quantiser +
+          AVX2 int8 dots, OpenMP), for half that time.
 """
 from __future__ import annotations
 
@@ -62,6 +64,7 @@ def parse():
     ap.add_argument("--gemm-m", type=int, nargs="*", default=[512, 2048])
     ap.add_argument("--batches", type=int, nargs="*", default=[2, 4, 8])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--repeats", type=int, default=20, help="replays timed one by one for median / p95")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--model-layers", type=int, default=64,
@@ -98,12 +101,38 @@ def cpu_baseline(seconds: float) -> dict:
             cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
     except (OSError, StopIteration):
         pass
+    # the integer path on the host: Q8_1 quantiser + int8 sub-block dots
+    # (AVX2) on every allowed core, same seven GEMVs, output equal to the
+    # kernel semantics
+    threads = max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS") or (os.cpu_count() or 1))))
+    i_bytes, i_passes, t1 = 0, 0, time.perf_counter()
+    while True:
+        for W, x, K, N in inputs:
+            orc.gemv_q8_1_host(W, x, K, N, threads)
+            i_bytes += gemv_bytes(K, N)
+        i_passes += 1
+        i_el = time.perf_counter() - t1
+        if i_el >= seconds / 2:
+            break
+    step_mb = sum(gemv_bytes(K, N) for _, K, N in SHAPES) / 1e6
     return {"value": round(done_bytes / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
             "sample": f"{passes} pass(es) of the 7 bs=1 projection GEMVs of one layer "
-                      f"({sum(gemv_bytes(K, N) for _, K, N in SHAPES) / 1e6:.1f} MB each), FP64 oracle "
+                      f"({step_mb:.1f} MB each), FP64 oracle "
                       f"{'kernels/matmul_iq4xs/ref_cpu.cpp' if kind == 'reference' else 'oracle/iq4xs_oracle.c'}, "
                       f"{el:.1f} s on '{cpu}' ({os.cpu_count()} logical cpus visible)",
-            "ms_per_step": round(el / passes * 1e3, 2)}
+            "ms_per_step": round(el / passes * 1e3, 2),
+            "int8_host": {"value": round(i_bytes / i_el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+                          "ms_per_step": round(i_el / i_passes * 1e3, 2),
+                          "sample": f"{i_passes} pass(es) of the same 7 GEMVs through oracle orc_gemv_q8_1_host "
+                                    f"(Q8_1 quantiser + AVX2 int8 sub-block dots, OpenMP over rows, {threads} "
+                                    f"threads; output bit-identical to the kernel semantics), {i_el:.1f} s"}}
+
+
+def spread(samples, name: str) -> dict:
+    """Median and 95th percentile of repeated timings (one graph replay each)."""
+    v = sorted(samples)
+    p95 = v[min(len(v) - 1, int(0.95 * len(v) + 0.5) - 1)] if v else None
+    return {"repeats": len(v), f"median_{name}": round(v[len(v) // 2], 4), f"p95_{name}": round(p95, 4)}
 
 
 class Timer:
@@ -319,6 +348,7 @@ def main() -> int:
     steps = reps * args.layers
     ms_per_step = us_total / steps / 1e3
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    step_stats = spread([timer(run, 1) / args.layers / 1e3 for _ in range(args.repeats)], "ms_per_step")
 
     # ---- roofline: the GEMV kernel alone on prequantised activations --------
     def gemv_rotation(wsb, yb, M) -> None:
@@ -332,6 +362,7 @@ def main() -> int:
     grun, _ = capture(torch, stream, lambda: gemv_rotation(wss, ys, 1), use_graph)
     timer(grun, 2)
     gemv_us = timer(grun, args.roofline_reps) / args.roofline_reps
+    launch_stats = spread([timer(grun, 1) / n_launch for _ in range(args.repeats)], "launch_us")
     avg_launch_us = gemv_us / n_launch
     achieved = step_bytes * args.layers / (gemv_us * 1e-6) / 1e9
     traffic = None
@@ -500,11 +531,13 @@ def main() -> int:
                                "(fp32 activations quantised to Q8_1 inside each call), weights HBM-resident",
                    "shapes_KxN": {n: [K, N] for n, K, N in SHAPES}, "batch": 1,
                    "layers_rotated": args.layers, "weight_bytes_resident": step_bytes * args.layers,
-                   "launch": launch, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+                   "launch": launch, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+                   "step_spread": step_stats},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "gemv_tile_kernel<1,2,false,false,false> (bs=1, prequantised Q8_1)",
-                     "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps},
+                     "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps,
+                     "launch_spread": launch_stats},
         "grouped_gemv": grouped,
         "small_batch_gemv": small,
         "gemm": {"peak_tops": INT8_PEAK_TOPS, "by_M": gemm,

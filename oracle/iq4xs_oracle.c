@@ -7,7 +7,9 @@
  */
 #include "iq4xs_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #ifdef _OPENMP
@@ -403,7 +405,6 @@ void orc_gemm_fp64(const orc_block_iq4_xs* W, const float* X, float* Y, int64_t 
             Y[n * M + m] = (float)row_dot_fp64(W + n * bpr, X + m, (ptrdiff_t)M, bpr);
 }
 
-/* kernels/matmul_iq4xs/ref_cpu.cpp:108-139 -- fp32 dequantisation. */
 /*
  * impl_gemv_gfx1100.hip:6-93 -- the FP64 GEMV of the
  * reference's gfx1100 kernel: the products of ref_cpu.cpp, summed as 8
@@ -435,6 +436,82 @@ void orc_gemv_fp64_by_subblock(const orc_block_iq4_xs* W, const float* x, float*
     }
 }
 
+/*
+ * Host int8 path (real_stock_dp4a_comparator.hip:230-264 quantiser, :145-166
+ * sub-block dot, :325-360 GEMV order), for timing the CPU against the GPU on
+ * the same integer semantics: x is quantised to Q8_1, each sub-block's codes
+ * are decoded with a byte shuffle and dotted against the Q8_1 codes in 16-bit
+ * lanes (exact: |kv * q| <= 16129), eight sub-block sums are reduced
+ * together, and the fp32 terms (fp16(d_w) * fp16(d_x)) * float(sumi * (ls-32))
+ * are added in orc_gemv_semantics' lane order -- so y is bit-identical to it.
+ * Rows are split over nthreads OpenMP threads.
+ */
+__attribute__((target("avx2"))) static inline __m256i dot_subblock_avx2(const uint8_t* qs16, const int8_t* a32,
+                                                                         __m128i table) {
+    const __m128i q = _mm_loadu_si128((const __m128i*)qs16);
+    const __m128i m4 = _mm_set1_epi8(0x0F);
+    const __m128i wl = _mm_shuffle_epi8(table, _mm_and_si128(q, m4));
+    const __m128i wh = _mm_shuffle_epi8(table, _mm_and_si128(_mm_srli_epi16(q, 4), m4));
+    const __m128i al = _mm_loadu_si128((const __m128i*)a32);
+    const __m128i ah = _mm_loadu_si128((const __m128i*)(a32 + 16));
+    const __m256i pl = _mm256_madd_epi16(_mm256_cvtepi8_epi16(wl), _mm256_cvtepi8_epi16(al));
+    const __m256i ph = _mm256_madd_epi16(_mm256_cvtepi8_epi16(wh), _mm256_cvtepi8_epi16(ah));
+    return _mm256_add_epi32(pl, ph);
+}
+
+__attribute__((target("avx2"))) void orc_gemv_q8_1_host(const orc_block_iq4_xs* W, const float* x, float* y,
+                                                        int64_t K, int64_t N, int nthreads) {
+    const int64_t bpr = K / ORC_QK_K, nb = K / ORC_QK8_1;
+    orc_block_q8_1* AQ = (orc_block_q8_1*)malloc((size_t)nb * sizeof(orc_block_q8_1));
+    float* dx = (float*)malloc((size_t)nb * sizeof(float));
+    int8_t* codes = (int8_t*)malloc((size_t)K);
+    orc_quantize_q8_1(x, AQ, K);
+    for (int64_t i = 0; i < nb; ++i) {
+        dx[i] = orc_fp16_to_fp32((uint16_t)(AQ[i].ds & 0xFFFFu));
+        memcpy(codes + i * ORC_QK8_1, AQ[i].qs, ORC_QK8_1);
+    }
+    const __m128i table = _mm_loadu_si128((const __m128i*)orc_kvalues_iq4nl);
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1)
+    {
+        float* T = (float*)malloc((size_t)nb * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < N; ++r) {
+            for (int64_t b = 0; b < bpr; ++b) {
+                const orc_block_iq4_xs* blk = W + r * bpr + b;
+                const int8_t* a = codes + b * ORC_QK_K;
+                __m256i v[8];
+                for (int ib = 0; ib < 8; ++ib) v[ib] = dot_subblock_avx2(blk->qs + 16 * ib, a + 32 * ib, table);
+                const __m256i h0 = _mm256_hadd_epi32(_mm256_hadd_epi32(v[0], v[1]), _mm256_hadd_epi32(v[2], v[3]));
+                const __m256i h1 = _mm256_hadd_epi32(_mm256_hadd_epi32(v[4], v[5]), _mm256_hadd_epi32(v[6], v[7]));
+                const __m256i s8 = _mm256_add_epi32(_mm256_permute2x128_si256(h0, h1, 0x20),
+                                                    _mm256_permute2x128_si256(h0, h1, 0x31));
+                int32_t ls[8];
+                for (int ib = 0; ib < 8; ++ib) ls[ib] = orc_subblock_scale(blk, ib) - 32;
+                const __m256i sumi = _mm256_mullo_epi32(s8, _mm256_loadu_si256((const __m256i*)ls));
+                const __m256 d = _mm256_mul_ps(_mm256_set1_ps(orc_fp16_to_fp32(blk->d)), _mm256_loadu_ps(dx + 8 * b));
+                _mm256_storeu_ps(T + 8 * b, _mm256_mul_ps(d, _mm256_cvtepi32_ps(sumi)));
+            }
+            float tmp[32];
+            for (int t = 0; t < 32; ++t) {
+                float acc = 0.0f;
+                for (int64_t kbx = t / 8; kbx < bpr; kbx += 4) acc += T[kbx * 8 + t % 8];
+                tmp[t] = acc;
+            }
+            for (int off = 16; off > 0; off >>= 1) {
+                float nt[32];
+                for (int t = 0; t < 32; ++t) nt[t] = tmp[t] + tmp[t ^ off];
+                memcpy(tmp, nt, sizeof nt);
+            }
+            y[r] = tmp[0];
+        }
+        free(T);
+    }
+    free(AQ);
+    free(dx);
+    free(codes);
+}
+
+/* kernels/matmul_iq4xs/ref_cpu.cpp:108-139 -- fp32 dequantisation. */
 void orc_dequant(const orc_block_iq4_xs* W, float* out, int64_t K, int64_t N) {
     const int64_t bpr = K / ORC_QK_K;
     for (int64_t r = 0; r < N; ++r)

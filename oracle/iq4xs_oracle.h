@@ -32,6 +32,8 @@
  *                             orc_quantize_q8_1 of the returned values
  *   orc_swiglu_q8_1           values vs float64 silu(g)*u, blocks through
  *                             orc_quantize_q8_1 of the returned values
+ *   orc_gemv_q8_1_host        bit-identical to orc_quantize_q8_1 +
+ *                             orc_gemv_semantics (tests/test_oracle.py)
  *   orc_gemv_semantics        fp32 summation ORDER of the gfx1100 kernel is
  *   orc_gemm_semantics        parity unpinned (no gfx1100 here); the integer
  *                             terms are pinned by orc_subblock_sums and the
@@ -95,6 +97,9 @@ void orc_gemm_fp64(const orc_block_iq4_xs* W, const float* X, float* Y, int64_t 
                    int64_t M, int nthreads);
 void orc_dequant(const orc_block_iq4_xs* W, float* out, int64_t K, int64_t N);
 void orc_gemv_fp64_by_subblock(const orc_block_iq4_xs* W, const float* x, float* y, int64_t K, int64_t N);
+/* Host int8 timing path: quantise x, then the GEMV; bit-identical to
+ * orc_gemv_semantics on the quantised x.  AVX2, nthreads OpenMP threads. */
+void orc_gemv_q8_1_host(const orc_block_iq4_xs* W, const float* x, float* y, int64_t K, int64_t N, int nthreads);
 
 /*
  * Fused producers -> Q8_1 (no counterpart in the reference's kernels; they

@@ -69,6 +69,7 @@ class Oracle:
             "orc_gemm_fp64": (None, [_P, _P, _P, _I64, _I64, _I64, ctypes.c_int]),
             "orc_dequant": (None, [_P, _P, _I64, _I64]),
             "orc_gemv_fp64_by_subblock": (None, [_P, _P, _P, _I64, _I64]),
+            "orc_gemv_q8_1_host": (None, [_P, _P, _P, _I64, _I64, ctypes.c_int]),
             "orc_exp_cw": (ctypes.c_float, [ctypes.c_float]),
             "orc_silu": (ctypes.c_float, [ctypes.c_float]),
             "orc_swiglu_q8_1": (None, [_P, _P, _I64, _I64, _P, _P]),
@@ -177,6 +178,14 @@ class Oracle:
         Y = np.empty((N, M), np.float32)
         self.lib.orc_gemm_semantics(_ptr(W), _ptr(AQ), _ptr(Y), K, N, M)
         return Y
+
+    def gemv_q8_1_host(self, W: np.ndarray, x: np.ndarray, K: int, N: int, nthreads: int = 1) -> np.ndarray:
+        """Host int8 path (quantise + GEMV) on nthreads threads; equals
+        gemv_semantics(W, quantize_q8_1(x)) bit for bit."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(N, np.float32)
+        self.lib.orc_gemv_q8_1_host(_ptr(W), _ptr(x), _ptr(y), K, N, nthreads)
+        return y
 
     def gemv_fp64(self, W: np.ndarray, x: np.ndarray, K: int, N: int) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)

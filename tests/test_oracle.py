@@ -468,3 +468,15 @@ def test_fp64_by_subblock_order_is_distinguishable(orc):
     x[0], x[32], x[256] = 2.0 ** 80, 1.0, -(2.0 ** 80)
     assert np.array_equal(orc.gemv_fp64(W, x, K, N), np.zeros(N, np.float32))
     assert np.array_equal(orc.gemv_fp64_by_subblock(W, x, K, N), np.ones(N, np.float32))
+
+
+@pytest.mark.parametrize("K,N,threads", [(256, 5, 1), (768, 37, 4), (5120, 64, 3), (2048, 1, 8)])
+def test_host_int8_path_equals_kernel_semantics(orc, K, N, threads):
+    """The host int8 timing path (byte-shuffle decode, 16-bit products, eight
+    sub-blocks reduced together, OpenMP rows) gives exactly the kernel
+    semantics on the quantised activations, for any thread count."""
+    W = orc.gen_weights(K, N, seed=K + N)
+    x = orc.gen_activations(K, seed=N, outliers=True)
+    want = orc.gemv_semantics(W, orc.quantize_q8_1(x), K, N)
+    got = orc.gemv_q8_1_host(W, x, K, N, threads)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
