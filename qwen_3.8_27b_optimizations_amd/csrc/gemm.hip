@@ -9,13 +9,22 @@
 // gemm_iq4xs_db_kernel (128x128 tile, 16 waves, double-buffered LDS) and
 // gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves, four per CU).
 //
-// Both are VALU-issue bound: the fp32 scaling costs 3 VALU ops per output and
-// sub-block (convert, scale product, fused add) against 1/16 of a 32x32x32
-// int8 MFMA.  Measured on the 128x128 kernel: removing the int8 MFMA changes
-// little, every VALU op removed shows up in full, forming the scale product
-// with an f32 MFMA (32x32x2, a rank-1 outer product) costs as much as the 16
-// multiplies it replaces, and keeping (ls - 32) as int8 with d_w applied once
-// per super-block (exact int32 sumi*(ls-32)) is 4-8 % slower.
+// Both are VALU-issue bound.  Every output needs its own scale per sub-block,
+// d_w[n] * d_x[m], so the epilogue costs VALU work per output and sub-block
+// against 1/16 of a 32x32x32 int8 MFMA per lane.  The scale tile is formed by
+// a bf16 MFMA from exact hi/lo splits of the two scales (scale_outer), which
+// leaves 2 VALU ops per output and sub-block (convert, fused add) instead of
+// 3 and removes the per-lane row-scale LDS reads: in the 128x128 kernel 8-20 %
+// faster than the multiply version; the 64x64 kernel keeps the multiplies,
+// which measured 5-10 % faster there.  Measured on the 128x128 kernel before that: removing the
+// int8 MFMA changed little and every VALU op removed showed up in full; an
+// f32 MFMA (32x32x2) for the same outer product cost as much as the 16
+// multiplies; keeping (ls - 32) as int8 with d_w applied once per super-block
+// (exact int32 sumi*(ls-32)) was 4-8 % slower.
+//
+// In the 128x128 kernel, non-finite scales (an fp16 d of Inf/NaN) give NaN
+// where the reference's product would give +-Inf: the hi/lo split of an
+// infinite scale is Inf + NaN.
 //
 // MI355X mapping (64x64 kernel).  A workgroup (4 waves) owns a 64-row x
 // 64-token output tile and walks K one 256-weight super-block at a time:
@@ -47,6 +56,31 @@ __device__ inline int lds_swz(int row, int chunk) { return row * 256 + ((chunk ^
 //   B: lane l supplies column (l & 31), k = 16*(l >> 5) .. +15
 //   C: element e of lane l is row 8*(e>>2) + 4*(l>>5) + (e&3), column (l & 31)
 __device__ inline int mfma_c_row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// x = hi + lo exactly, as two bf16 halves (hi | lo << 16), for any finite x
+// with at most 16 significant bits: d_w * (ls - 32) (11 + 5 bits) and the
+// fp16 d_x both qualify.  hi keeps the top 8 bits, lo the rest.
+__device__ inline uint32_t bf16_pair(float x) {
+    const uint32_t hb = __builtin_bit_cast(uint32_t, x) & 0xFFFF0000u;
+    const float lo = x - __builtin_bit_cast(float, hb);
+    return (hb >> 16) | (__builtin_bit_cast(uint32_t, lo) & 0xFFFF0000u);
+}
+
+// Scale product d_w[row] * d_x[col] of every element of a 32x32 tile, in the
+// int8 MFMA's C layout, from one v_mfma_f32_32x32x8_bf16.  pa is the bf16 pair
+// of this lane's row scale (0 on lanes 32-63, which supply k = 4..7), pb that
+// of its column's.  k = 0..3 carry hi*hi, lo*hi, hi*lo, lo*lo: four products
+// exact in fp32, so the tile holds d_w * d_x to within fp32 rounding of their
+// sum.  It replaces 16 multiplies and 16 row-scale LDS reads per lane.
+__device__ inline v16f scale_outer(uint32_t pa, uint32_t pb) {
+    const v2u av = {pa, pa};                                                // hi, lo, hi, lo
+    const v2u bv = {__builtin_amdgcn_perm(pb, pb, 0x01000100u), __builtin_amdgcn_perm(pb, pb, 0x03020302u)};  // hi, hi, lo, lo
+    return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4s, av), __builtin_bit_cast(v4s, bv), v16f{},
+                                                    0, 0, 0);
+}
 
 template <bool kDebug>
 __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __restrict__ W,
@@ -110,7 +144,8 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
         }
         __syncthreads();
 
-        // 3. one MFMA per sub-block, fp32 scale epilogue
+        // 3. one MFMA per sub-block, fp32 scale epilogue (the bf16 scale tile of
+        //    the 128x128 kernel measured 5-10 % slower in this one)
         const int ra = 32 * wn + (lane & 31);
         const int rb = 32 * wm + (lane & 31);
 #pragma unroll 2
@@ -159,8 +194,8 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
 constexpr int G2_BN = 128, G2_BM = 128, G2_THREADS = 1024;
 constexpr int G2_ROW = 272;                                  // padded LDS row (256 codes + 16)
 constexpr int G2_W_BYTES = G2_BN * G2_ROW, G2_X_BYTES = G2_BM * G2_ROW;
-constexpr int G2_SA_OFF = G2_W_BYTES + G2_X_BYTES;         // float [8][128]
-constexpr int G2_SB_OFF = G2_SA_OFF + 8 * G2_BN * 4;        // float [8][128]
+constexpr int G2_SA_OFF = G2_W_BYTES + G2_X_BYTES;         // uint32 [8][128]: bf16 pairs of d_w * (ls - 32)
+constexpr int G2_SB_OFF = G2_SA_OFF + 8 * G2_BN * 4;        // uint32 [8][128]: bf16 pairs of d_x
 constexpr int G2_SL_OFF = G2_SB_OFF + 8 * G2_BM * 4;        // int8  [8][128] (debug only)
 constexpr int G2_STAGE = G2_SL_OFF;                          // bytes per stage without the debug table
 constexpr int G2_STAGE_DBG = G2_SL_OFF + 8 * G2_BN;
@@ -222,12 +257,13 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
         *reinterpret_cast<v4i*>(wdst) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
         *reinterpret_cast<v4i*>(wdst + 16) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         const int ls = subblock_ls(g.wh.x, g.wh.y, wsb) - 32;
-        reinterpret_cast<float*>(base + G2_SA_OFF)[wsb * G2_BN + wr] = half_bits_to_float(g.wh.x & 0xFFFFu) * (float)ls;
+        reinterpret_cast<uint32_t*>(base + G2_SA_OFF)[wsb * G2_BN + wr] =
+            bf16_pair(half_bits_to_float(g.wh.x & 0xFFFFu) * (float)ls);
         if (kDebug) reinterpret_cast<int8_t*>(base + G2_SL_OFF)[wsb * G2_BN + wr] = (int8_t)ls;
 #pragma unroll
         for (int it = 0; it < 2; ++it)
             *reinterpret_cast<v4i*>(base + G2_W_BYTES + xr[it] * G2_ROW + 16 * xc[it]) = g.x[it];
-        reinterpret_cast<float*>(base + G2_SB_OFF)[ds_s * G2_BM + dr] = half_bits_to_float(g.ds & 0xFFFFu);
+        reinterpret_cast<uint32_t*>(base + G2_SB_OFF)[ds_s * G2_BM + dr] = bf16_pair(half_bits_to_float(g.ds & 0xFFFFu));
     };
 
     float acc[16];
@@ -236,6 +272,7 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
     const int ra = 32 * wn + (lane & 31);
     const int rb = 32 * wm + (lane & 31);
     const int half = lane >> 5;  // k = 16*half .. +15 of each 32-wide sub-block
+    const uint32_t hmask = half ? 0u : 0xFFFFFFFFu;  // the scale MFMA's k = 4..7 are zero
 
     GemmPref g;
     load(g, 0);
@@ -248,21 +285,17 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
         const uint8_t* base = lds + cur * kStage;
         const int8_t* pa = reinterpret_cast<const int8_t*>(base) + ra * G2_ROW + 16 * half;
         const int8_t* pb = reinterpret_cast<const int8_t*>(base + G2_W_BYTES) + rb * G2_ROW + 16 * half;
-        const float* pA = reinterpret_cast<const float*>(base + G2_SA_OFF) + 32 * wn + 4 * half;
-        const float* pB = reinterpret_cast<const float*>(base + G2_SB_OFF) + rb;
+        const uint32_t* pA = reinterpret_cast<const uint32_t*>(base + G2_SA_OFF) + ra;
+        const uint32_t* pB = reinterpret_cast<const uint32_t*>(base + G2_SB_OFF) + rb;
 #pragma unroll 2
         for (int s = 0; s < 8; ++s) {
             const v4i a = *reinterpret_cast<const v4i*>(pa + 32 * s);
             const v4i b = *reinterpret_cast<const v4i*>(pb + 32 * s);
-            // row scales of this lane's 16 elements: rows 8j + 4*half + 0..3
-            v4f sa[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sa[j] = *reinterpret_cast<const v4f*>(pA + s * G2_BN + 8 * j);
-            const float bx = pB[s * G2_BM];
+            const v16f sc = scale_outer(hmask & pA[s * G2_BN], pB[s * G2_BM]);
             const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                acc[e] += (sa[e >> 2][e & 3] * bx) * (float)c[e];
+                acc[e] += sc[e] * (float)c[e];
                 if (kDebug) {
                     const int i = 32 * wn + mfma_c_row(e, lane);
                     const int8_t* sL = reinterpret_cast<const int8_t*>(base + G2_SL_OFF);
