@@ -69,17 +69,23 @@ __device__ inline uint32_t bf16_pair(float x) {
     return (hb >> 16) | (__builtin_bit_cast(uint32_t, lo) & 0xFFFF0000u);
 }
 
-// Scale product d_w[row] * d_x[col] of every element of a 32x32 tile, in the
-// int8 MFMA's C layout, from one v_mfma_f32_32x32x8_bf16.  pa is the bf16 pair
-// of this lane's row scale (0 on lanes 32-63, which supply k = 4..7), pb that
-// of its column's.  k = 0..3 carry hi*hi, lo*hi, hi*lo, lo*lo: four products
-// exact in fp32, so the tile holds d_w * d_x to within fp32 rounding of their
-// sum.  It replaces 16 multiplies and 16 row-scale LDS reads per lane.
-__device__ inline v16f scale_outer(uint32_t pa, uint32_t pb) {
-    const v2u av = {pa, pa};                                                // hi, lo, hi, lo
-    const v2u bv = {__builtin_amdgcn_perm(pb, pb, 0x01000100u), __builtin_amdgcn_perm(pb, pb, 0x03020302u)};  // hi, hi, lo, lo
-    return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4s, av), __builtin_bit_cast(v4s, bv), v16f{},
-                                                    0, 0, 0);
+// Scale products d_w[row] * d_x[col] of every element of the 32x32 tiles of
+// two sub-blocks s, s+1, in the int8 MFMA's C layout, from two
+// v_mfma_f32_32x32x8_bf16.  pa holds the bf16 pairs of this lane's row scale
+// for s (low dword) and s+1 (high dword); pb0 / pb1 those of its column's.
+// Lane half h supplies k = 4h..4h+3: A = (w_hi, w_lo) of s, then of s+1; B =
+// x_hi (h = 0) or x_lo (h = 1) of s twice, then two zeros (for s; the other
+// way round for s+1), the copy picked by the per-lane selector bsel.  The four
+// nonzero products hi*hi, lo*hi, hi*lo, lo*lo are exact in fp32, so each tile
+// holds d_w * d_x to within fp32 rounding of their sum.  This replaces 16
+// multiplies and 16 row-scale LDS reads per lane and sub-block at one v_perm.
+__device__ inline void scale_outer2(v2u pa, uint32_t pb0, uint32_t pb1, uint32_t bsel, v16f& sc0, v16f& sc1) {
+    const v2u b0 = {__builtin_amdgcn_perm(pb0, pb0, bsel), 0u};
+    const v2u b1 = {0u, __builtin_amdgcn_perm(pb1, pb1, bsel)};
+    sc0 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4s, pa), __builtin_bit_cast(v4s, b0), v16f{}, 0,
+                                                   0, 0);
+    sc1 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4s, pa), __builtin_bit_cast(v4s, b1), v16f{}, 0,
+                                                   0, 0);
 }
 
 template <bool kDebug>
@@ -193,11 +199,16 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
 // offset from sub-block 0 (no per-sub-block address arithmetic).
 constexpr int G2_BN = 128, G2_BM = 128, G2_THREADS = 1024;
 constexpr int G2_ROW = 272;                                  // padded LDS row (256 codes + 16)
+// Stage layout: the two scale tables first, then the code tiles, so that every
+// read of the MFMA phase is a 16-bit immediate offset from the stage base.
 constexpr int G2_W_BYTES = G2_BN * G2_ROW, G2_X_BYTES = G2_BM * G2_ROW;
-constexpr int G2_SA_OFF = G2_W_BYTES + G2_X_BYTES;         // uint32 [8][128]: bf16 pairs of d_w * (ls - 32)
+constexpr int G2_SA_OFF = 0;                                 // uint32 [4][128][2]: bf16 pairs of d_w * (ls - 32)
 constexpr int G2_SB_OFF = G2_SA_OFF + 8 * G2_BN * 4;        // uint32 [8][128]: bf16 pairs of d_x
-constexpr int G2_SL_OFF = G2_SB_OFF + 8 * G2_BM * 4;        // int8  [8][128] (debug only)
+constexpr int G2_W_OFF = G2_SB_OFF + 8 * G2_BM * 4;         // int8 [128][272] weight codes
+constexpr int G2_X_OFF = G2_W_OFF + G2_W_BYTES;             // int8 [128][272] token codes
+constexpr int G2_SL_OFF = G2_X_OFF + G2_X_BYTES;            // int8  [8][128] (debug only)
 constexpr int G2_STAGE = G2_SL_OFF;                          // bytes per stage without the debug table
+static_assert(G2_X_OFF + 7 * 32 + 16 < 65536, "MFMA-phase LDS immediate offsets fit 16 bits");
 constexpr int G2_STAGE_DBG = G2_SL_OFF + 8 * G2_BN;
 
 struct GemmPref {
@@ -253,16 +264,16 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
         uint32_t lo[4], hi[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)g.wq[j], lo[j], hi[j]);
-        int8_t* wdst = reinterpret_cast<int8_t*>(base) + wr * G2_ROW + 32 * wsb;
+        int8_t* wdst = reinterpret_cast<int8_t*>(base + G2_W_OFF) + wr * G2_ROW + 32 * wsb;
         *reinterpret_cast<v4i*>(wdst) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
         *reinterpret_cast<v4i*>(wdst + 16) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         const int ls = subblock_ls(g.wh.x, g.wh.y, wsb) - 32;
-        reinterpret_cast<uint32_t*>(base + G2_SA_OFF)[wsb * G2_BN + wr] =
+        reinterpret_cast<uint32_t*>(base + G2_SA_OFF)[((wsb >> 1) * G2_BN + wr) * 2 + (wsb & 1)] =
             bf16_pair(half_bits_to_float(g.wh.x & 0xFFFFu) * (float)ls);
         if (kDebug) reinterpret_cast<int8_t*>(base + G2_SL_OFF)[wsb * G2_BN + wr] = (int8_t)ls;
 #pragma unroll
         for (int it = 0; it < 2; ++it)
-            *reinterpret_cast<v4i*>(base + G2_W_BYTES + xr[it] * G2_ROW + 16 * xc[it]) = g.x[it];
+            *reinterpret_cast<v4i*>(base + G2_X_OFF + xr[it] * G2_ROW + 16 * xc[it]) = g.x[it];
         reinterpret_cast<uint32_t*>(base + G2_SB_OFF)[ds_s * G2_BM + dr] = bf16_pair(half_bits_to_float(g.ds & 0xFFFFu));
     };
 
@@ -272,7 +283,7 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
     const int ra = 32 * wn + (lane & 31);
     const int rb = 32 * wm + (lane & 31);
     const int half = lane >> 5;  // k = 16*half .. +15 of each 32-wide sub-block
-    const uint32_t hmask = half ? 0u : 0xFFFFFFFFu;  // the scale MFMA's k = 4..7 are zero
+    const uint32_t bsel = half ? 0x03020302u : 0x01000100u;  // d_x lo (high half) or hi (low half), twice
 
     GemmPref g;
     load(g, 0);
@@ -283,24 +294,31 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
         const bool more = kb + 1 < bpr;
         if (more) load(g, kb + 1);  // in flight during the MFMA phase
         const uint8_t* base = lds + cur * kStage;
-        const int8_t* pa = reinterpret_cast<const int8_t*>(base) + ra * G2_ROW + 16 * half;
-        const int8_t* pb = reinterpret_cast<const int8_t*>(base + G2_W_BYTES) + rb * G2_ROW + 16 * half;
-        const uint32_t* pA = reinterpret_cast<const uint32_t*>(base + G2_SA_OFF) + ra;
+        const int8_t* pa = reinterpret_cast<const int8_t*>(base + G2_W_OFF) + ra * G2_ROW + 16 * half;
+        const int8_t* pb = reinterpret_cast<const int8_t*>(base + G2_X_OFF) + rb * G2_ROW + 16 * half;
+        // row-scale pairs of sub-blocks 2t, 2t+1 are adjacent dwords: the table
+        // is [4][128][2] (sub-block pair, row, member)
+        const v2u* pA = reinterpret_cast<const v2u*>(base + G2_SA_OFF) + ra;
         const uint32_t* pB = reinterpret_cast<const uint32_t*>(base + G2_SB_OFF) + rb;
-#pragma unroll 2
-        for (int s = 0; s < 8; ++s) {
-            const v4i a = *reinterpret_cast<const v4i*>(pa + 32 * s);
-            const v4i b = *reinterpret_cast<const v4i*>(pb + 32 * s);
-            const v16f sc = scale_outer(hmask & pA[s * G2_BN], pB[s * G2_BM]);
-            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
+#pragma unroll 1
+        for (int s = 0; s < 8; s += 2) {
+            v16f sc[2];
+            scale_outer2(pA[(s >> 1) * G2_BN], pB[s * G2_BM], pB[(s + 1) * G2_BM], bsel, sc[0], sc[1]);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                acc[e] += sc[e] * (float)c[e];
-                if (kDebug) {
-                    const int i = 32 * wn + mfma_c_row(e, lane);
-                    const int8_t* sL = reinterpret_cast<const int8_t*>(base + G2_SL_OFF);
-                    const int64_t m = m0 + rb;
-                    if (m < M && n0 + i < N) dbg[(m * N + n0 + i) * nb + kb * 8 + s] = c[e] * (int)sL[s * G2_BN + i];
+            for (int u = 0; u < 2; ++u) {
+                const v4i a = *reinterpret_cast<const v4i*>(pa + 32 * (s + u));
+                const v4i b = *reinterpret_cast<const v4i*>(pb + 32 * (s + u));
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    acc[e] += sc[u][e] * (float)c[e];
+                    if (kDebug) {
+                        const int i = 32 * wn + mfma_c_row(e, lane);
+                        const int8_t* sL = reinterpret_cast<const int8_t*>(base + G2_SL_OFF);
+                        const int64_t m = m0 + rb;
+                        if (m < M && n0 + i < N)
+                            dbg[(m * N + n0 + i) * nb + kb * 8 + s + u] = c[e] * (int)sL[(s + u) * G2_BN + i];
+                    }
                 }
             }
         }
