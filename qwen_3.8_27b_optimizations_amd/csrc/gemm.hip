@@ -236,28 +236,34 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
     const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
 
     // this thread's share of a super-block's loads (rows / tokens past the end
-    // are clamped to the last one; their results are never stored)
+    // are clamped to the last one; their results are never stored).  Each is a
+    // 32-bit lane offset from a workgroup-uniform base (the launcher bounds the
+    // tile's span below 2^32 bytes), which keeps the pointers out of VGPRs.
     const int wr = tid >> 3, wsb = tid & 7;  // weight row, sub-block
-    const uint8_t* wrow = W + ((n0 + wr < N) ? n0 + wr : N - 1) * row_bytes;
+    const uint8_t* wbase = W + n0 * row_bytes;
+    const uint32_t woff = (uint32_t)(((n0 + wr < N) ? wr : N - 1 - n0) * row_bytes);
     int xr[2], xc[2];
-    const int8_t* xrow[2];
+    uint32_t xoff[2];
+    const int8_t* xbase = aqs + m0 * K;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int p = tid + G2_THREADS * it;
         xr[it] = p >> 4;
         xc[it] = p & 15;
-        xrow[it] = aqs + ((m0 + xr[it] < M) ? m0 + xr[it] : M - 1) * K + 16 * xc[it];
+        xoff[it] = (uint32_t)(((m0 + xr[it] < M) ? xr[it] : M - 1 - m0) * K + 16 * xc[it]);
     }
     const int dr = tid >> 3, ds_s = tid & 7;  // token, sub-block of the d word
-    const uint32_t* drow = ads + ((m0 + dr < M) ? m0 + dr : M - 1) * nb + ds_s;
+    const uint32_t* dbase = ads + m0 * nb;
+    const uint32_t doff = (uint32_t)(((m0 + dr < M) ? dr : M - 1 - m0) * nb + ds_s);
 
     auto load = [&](GemmPref& g, int64_t kb) {
-        const uint8_t* blk = wrow + kb * BLOCK_BYTES;
-        g.wh = *reinterpret_cast<const v2u*>(blk);
-        g.wq = *reinterpret_cast<const v4i_a8*>(blk + 8 + 16 * wsb);
+        const uint8_t* wk = wbase + kb * BLOCK_BYTES;
+        g.wh = *reinterpret_cast<const v2u*>(wk + woff);
+        g.wq = *reinterpret_cast<const v4i_a8*>(wk + woff + 8 + 16 * wsb);
+        const int8_t* xk = xbase + kb * QK_K;
 #pragma unroll
-        for (int it = 0; it < 2; ++it) g.x[it] = *reinterpret_cast<const v4i*>(xrow[it] + kb * QK_K);
-        g.ds = drow[kb * 8];
+        for (int it = 0; it < 2; ++it) g.x[it] = *reinterpret_cast<const v4i*>(xk + xoff[it]);
+        g.ds = (dbase + kb * 8)[doff];
     };
     auto store = [&](const GemmPref& g, int stage) {
         uint8_t* base = lds + stage * kStage;
@@ -300,7 +306,7 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
         // is [4][128][2] (sub-block pair, row, member)
         const v2u* pA = reinterpret_cast<const v2u*>(base + G2_SA_OFF) + ra;
         const uint32_t* pB = reinterpret_cast<const uint32_t*>(base + G2_SB_OFF) + rb;
-#pragma unroll 1
+#pragma unroll 2
         for (int s = 0; s < 8; s += 2) {
             v16f sc[2];
             scale_outer2(pA[(s >> 1) * G2_BN], pB[s * G2_BM], pB[(s + 1) * G2_BM], bsel, sc[0], sc[1]);
@@ -361,7 +367,9 @@ static int gemm_cu_count() {
 // the 64x64 kernel (four per CU) wins when big tiles leave CUs idle: fewer
 // tiles than ~9/16 of the CUs, or a last round that is mostly empty
 // (thresholds from measurements on the 27B-class shapes at M = 512 / 2048).
-static bool use_big_tiles(int64_t N, int64_t M) {
+static bool use_big_tiles(int64_t N, int64_t M, int64_t K) {
+    // the 128x128 kernel addresses a tile's rows and tokens with 32-bit offsets
+    if ((int64_t)G2_BN * (K / QK_K) * BLOCK_BYTES >= (1ll << 32) || (int64_t)G2_BM * K >= (1ll << 32)) return false;
     const int k = gemm_kind();
     if (k == 0 || k == 1) return k == 1;
     const int64_t cus = gemm_cu_count();
@@ -374,7 +382,7 @@ static bool use_big_tiles(int64_t N, int64_t M) {
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     clear_launch_error();
-    if (use_big_tiles(N, M)) {
+    if (use_big_tiles(N, M, K)) {
         const int64_t gx = (N + G2_BN - 1) / G2_BN;
         const int64_t gy = (M + G2_BM - 1) / G2_BM;
         if (gx > 0x7FFFFFFF || gy > 65535) return hipErrorInvalidConfiguration;
