@@ -292,6 +292,15 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
                     "frac_of_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
                     "tokens_per_s": round(M / (us * 1e-6), 1), "finite": finite512(),
                     "includes": "the producers and the q re-quantisation of every layer"}
+    del prefill
+    prefill_g, finite512g = chain(M, grouped=True)
+    prefill_g()
+    torch.cuda.synchronize()
+    us = timer(prefill_g, 1)
+    out["bs512_grouped"] = {"ms_per_pass": round(us / 1e3, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+                            "frac_of_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+                            "tokens_per_s": round(M / (us * 1e-6), 1), "finite": finite512g(),
+                            "note": "same chain; q,k,v and gate,up each one iq4xs_mul_mat_q8_1_group launch"}
     return out
 
 
@@ -503,6 +512,45 @@ def main() -> int:
             del X, ws, Y
         tops = ops / (us_sum * 1e-6) / 1e12
         gemm[str(M)] = {"tops": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4), "per_shape_us": per_shape}
+        # the same seven projections with q,k,v and gate,up as one grouped launch each
+        import ctypes
+
+        K0 = SHAPES[0][1]
+        X = pkg.synthetic_activations(K0 * M, seed=300, device=dev)
+        ws = pkg.quantize_q8_1(X, K0, M)
+        Xo = pkg.synthetic_activations(SHAPES[3][1] * M, seed=303, device=dev)
+        wso = pkg.quantize_q8_1(Xo, SHAPES[3][1], M)
+        Xd = pkg.synthetic_activations(SHAPES[6][1] * M, seed=306, device=dev)
+        wsd = pkg.quantize_q8_1(Xd, SHAPES[6][1], M)
+        Ys = [torch.empty((M, N), device=dev) for (_, _, N) in SHAPES]
+
+        def gargs(l, idx):
+            n = len(idx)
+            return (n, (ctypes.c_void_p * n)(*[layers[l][i].data_ptr() for i in idx]),
+                    (ctypes.c_void_p * n)(*[Ys[i].data_ptr() for i in idx]),
+                    (ctypes.c_int64 * n)(*[SHAPES[i][2] for i in idx]))
+
+        ga = [(gargs(l, [0, 1, 2]), gargs(l, [4, 5])) for l in range(args.layers)]
+        gctr = [0]
+
+        def grouped_layer():
+            l = gctr[0] % args.layers
+            gctr[0] += 1
+            (n, wp, yp, nn), (n2, wp2, yp2, nn2) = ga[l]
+            L.check("iq4xs_mul_mat_q8_1_group", n, wp, yp, nn, ws.data_ptr(), K0, M, pkg.LAYOUT_MK, s)
+            pkg.mul_mat_q8_1(layers[l][3], wso, SHAPES[3][1], SHAPES[3][2], M, out=Ys[3])
+            L.check("iq4xs_mul_mat_q8_1_group", n2, wp2, yp2, nn2, ws.data_ptr(), K0, M, pkg.LAYOUT_MK, s)
+            pkg.mul_mat_q8_1(layers[l][6], wsd, SHAPES[6][1], SHAPES[6][2], M, out=Ys[6])
+
+        for _ in range(2):
+            grouped_layer()
+        nrep = 4 if M >= 2048 else 8
+        g_us = timer(grouped_layer, nrep) / nrep
+        gemm[str(M)]["grouped"] = {"tops": round(ops / (g_us * 1e-6) / 1e12, 2),
+                                   "frac": round(ops / (g_us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+                                   "us_per_layer": round(g_us, 1),
+                                   "note": "q,k,v and gate,up each one iq4xs_mul_mat_q8_1_group launch; o, down alone"}
+        del X, ws, Xo, wso, Xd, wsd, Ys
 
     # ---- whole-model weight stream (64 distinct layers resident) -----------
     model = None

@@ -207,10 +207,12 @@ int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64
 
 /* Several weight matrices (1 <= count <= 4, each N[i] x K) against the same
  * quantised activations in ws: Y[i] = W[i] * dequant(ws), Y[i] laid out as
- * `layout` selects.  For M <= 8 one GEMV launch covers every matrix (q/k/v,
- * gate/up of a decode step), which pays the per-launch fixed cost once; each
- * output is bit-identical to iq4xs_mul_mat_q8_1 on its own matrix.  M > 8
- * runs the GEMM per matrix.  W, Y, N are host arrays of count entries.  No
+ * `layout` selects.  One launch covers every matrix: for M <= 8 the GEMV
+ * (q/k/v, gate/up of a decode step), which pays the per-launch fixed cost
+ * once; for M > 8 the GEMM, whose small matrices then fill the CUs that the
+ * big ones' last round of tiles leaves idle.  Each output is bit-identical to
+ * iq4xs_mul_mat_q8_1 (path AUTO) on its own matrix.  W, Y, N are host arrays
+ * of count entries.  No
  * counterpart in the reference, which runs every projection as its own
  * mul_mat. */
 int iq4xs_mul_mat_q8_1_group(int count, const void* const* W, float* const* Y, const int64_t* N, const void* ws,

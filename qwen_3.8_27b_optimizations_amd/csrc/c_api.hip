@@ -266,17 +266,11 @@ int iq4xs_mul_mat_q8_1_group(int count, const void* const* W, float* const* Y, c
     if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
     for (int i = 0; i < count; ++i)
         if (!valid_mat(W[i], ws, Y[i], K, N[i], M)) return hipErrorInvalidValue;
-    if (M > GEMV_MAX_COLS) {  // the GEMM already fills the chip per matrix
-        for (int i = 0; i < count; ++i) {
-            const hipError_t e = mul_mat_planar(static_cast<const uint8_t*>(W[i]), ws, Y[i], K, N[i], M, layout,
-                                                IQ4XS_PATH_GEMM, nullptr, as_stream(stream));
-            if (e != hipSuccess) return e;
-        }
-        return hipSuccess;
-    }
     const Planar p = planar_view(ws, K, M);
     const uint8_t* Wb[GEMV_GROUP_MAX];
     for (int i = 0; i < count; ++i) Wb[i] = static_cast<const uint8_t*>(W[i]);
+    if (M > GEMV_MAX_COLS)  // one GEMM launch: small matrices fill the big ones' last round
+        return launch_gemm_group(count, Wb, Y, N, p.qs, p.ds, K, M, layout == LAYOUT_MK, as_stream(stream));
     return launch_gemv_group(count, Wb, Y, N, p.qs, p.ds, K, M, layout == LAYOUT_MK, as_stream(stream));
 }
 

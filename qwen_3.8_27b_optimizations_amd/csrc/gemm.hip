@@ -15,27 +15,29 @@
 // a bf16 MFMA from exact hi/lo splits of the two scales (scale_outer), which
 // leaves 2 VALU ops per output and sub-block (convert, fused add) instead of
 // 3 and removes the per-lane row-scale LDS reads: in the 128x128 kernel 8-20 %
-// faster than the multiply version; the 64x64 kernel keeps the multiplies,
-// which measured 5-10 % faster there.  Measured on the 128x128 kernel before that: removing the
+// faster than the multiply version.  The 64x64 kernel measured 3-5 % slower
+// with it than with the multiplies, but uses it too: both kernels then give
+// bit-identical outputs, so the tile choice (which depends on the shape, and
+// for grouped launches on the group) never changes a result.  Measured on the 128x128 kernel before that: removing the
 // int8 MFMA changed little and every VALU op removed showed up in full; an
 // f32 MFMA (32x32x2) for the same outer product cost as much as the 16
 // multiplies; keeping (ls - 32) as int8 with d_w applied once per super-block
 // (exact int32 sumi*(ls-32)) was 4-8 % slower.
 //
-// In the 128x128 kernel, non-finite scales (an fp16 d of Inf/NaN) give NaN
-// where the reference's product would give +-Inf: the hi/lo split of an
-// infinite scale is Inf + NaN.
+// Non-finite scales (an fp16 d of Inf/NaN) give NaN where the reference's
+// product would give +-Inf: the hi/lo split of an infinite scale is Inf + NaN.
 //
 // MI355X mapping (64x64 kernel).  A workgroup (4 waves) owns a 64-row x
 // 64-token output tile and walks K one 256-weight super-block at a time:
 //   1. the 64 weight rows' super-blocks are decoded (v_perm codebook lookup,
 //      decode_codes_x)
 //      straight into int8 LDS tiles, the per-sub-block weight scales
-//      d*(ls-32) into a float table;
-//   2. the 64 tokens' Q8_1 codes are copied to LDS, their d into a table;
+//      d*(ls-32) into a table of exact bf16 hi/lo pairs (bf16_pair);
+//   2. the 64 tokens' Q8_1 codes are copied to LDS, their d into a pair table;
 //   3. each wave issues one v_mfma_i32_32x32x32_i8 per 32-wide sub-block --
 //      K=32 is exactly one sub-block, so the MFMA result IS the reference's
-//      int32 sumi -- and folds it into fp32 accumulators with the two scales.
+//      int32 sumi -- and folds it into fp32 accumulators with the scale tile
+//      of scale_outer2.
 // LDS rows are 256 bytes; the 16-byte chunk index is XORed with (row & 15)
 // so the 32 lanes that read one k-chunk of 32 different rows hit 16
 // distinct chunk positions (no bank conflicts from the 256-byte row stride).
@@ -56,6 +58,44 @@ __device__ inline int lds_swz(int row, int chunk) { return row * 256 + ((chunk ^
 //   B: lane l supplies column (l & 31), k = 16*(l >> 5) .. +15
 //   C: element e of lane l is row 8*(e>>2) + 4*(l>>5) + (e&3), column (l & 31)
 __device__ inline int mfma_c_row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
+
+// Up to GEMV_GROUP_MAX matrices with the same K and the same quantised
+// activations, run by one launch: the N-tiles of matrix i are blockIdx.x in
+// [tile_end[i-1], tile_end[i]).  Single-matrix launches use entry 0 only.
+struct GemmGroup {
+    const uint8_t* W[GEMV_GROUP_MAX];
+    float* Y[GEMV_GROUP_MAX];
+    int64_t N[GEMV_GROUP_MAX];
+    int64_t ldy_m[GEMV_GROUP_MAX];
+    int tile_end[GEMV_GROUP_MAX];
+};
+
+// This workgroup's matrix and its first N-tile, by scalar selects on the
+// by-value descriptor (no dynamic index into the argument block).
+template <bool kGroup>
+__device__ inline void gemm_select(const GemmGroup& grp, const uint8_t*& W, float*& Y, int64_t& N, int64_t& ldy_m,
+                                   int& tile0) {
+    W = grp.W[0];
+    Y = grp.Y[0];
+    N = grp.N[0];
+    ldy_m = grp.ldy_m[0];
+    tile0 = 0;
+    if (kGroup) {
+        int g = 0;
+#pragma unroll
+        for (int i = 0; i + 1 < GEMV_GROUP_MAX; ++i) g += (int)blockIdx.x >= grp.tile_end[i] ? 1 : 0;
+#pragma unroll
+        for (int i = 1; i < GEMV_GROUP_MAX; ++i) {
+            if (g == i) {
+                W = grp.W[i];
+                Y = grp.Y[i];
+                N = grp.N[i];
+                ldy_m = grp.ldy_m[i];
+                tile0 = grp.tile_end[i - 1];
+            }
+        }
+    }
+}
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -88,24 +128,26 @@ __device__ inline void scale_outer2(v2u pa, uint32_t pb0, uint32_t pb1, uint32_t
                                                    0, 0);
 }
 
-template <bool kDebug>
-__global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __restrict__ W,
-                                                              const int8_t* __restrict__ aqs,
-                                                              const uint32_t* __restrict__ ads,
-                                                              float* __restrict__ Y, int64_t K, int64_t N,
-                                                              int64_t M, int64_t ldy_m, int64_t ldy_n,
-                                                              int32_t* __restrict__ dbg) {
+template <bool kDebug, bool kGroup>
+__global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const GemmGroup grp, const int8_t* __restrict__ aqs,
+                                                              const uint32_t* __restrict__ ads, int64_t K, int64_t M,
+                                                              int64_t ldy_n, int32_t* __restrict__ dbg) {
     __shared__ __attribute__((aligned(16))) int8_t sW[GEMM_BN * 256];
     __shared__ __attribute__((aligned(16))) int8_t sX[GEMM_BM * 256];
-    __shared__ __attribute__((aligned(16))) float sA[8][GEMM_BN];
-    __shared__ __attribute__((aligned(16))) float sB[8][GEMM_BM];
+    __shared__ __attribute__((aligned(16))) uint32_t sA[4][GEMM_BN][2];  // bf16 pairs of d_w * (ls - 32), sub-block pairs
+    __shared__ __attribute__((aligned(16))) uint32_t sB[8][GEMM_BM];     // bf16 pairs of d_x
     __shared__ int sL[kDebug ? 8 : 1][GEMM_BN];  // ls - 32, only for the debug export
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wn = wave & 1, wm = wave >> 1;
-    const int64_t n0 = (int64_t)blockIdx.x * GEMM_BN;
+    const uint8_t* W;
+    float* Y;
+    int64_t N, ldy_m;
+    int tile0;
+    gemm_select<kGroup>(grp, W, Y, N, ldy_m, tile0);
+    const int64_t n0 = (int64_t)((int)blockIdx.x - tile0) * GEMM_BN;
     const int64_t m0 = (int64_t)blockIdx.y * GEMM_BM;
     const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
 
@@ -129,7 +171,7 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
             for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)w[j], lo[j], hi[j]);
             *reinterpret_cast<v4i*>(sW + lds_swz(r, 2 * s)) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
             *reinterpret_cast<v4i*>(sW + lds_swz(r, 2 * s + 1)) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-            sA[s][r] = half_bits_to_float(h.x & 0xFFFFu) * (float)(subblock_ls(h.x, h.y, s) - 32);
+            sA[s >> 1][r][s & 1] = bf16_pair(half_bits_to_float(h.x & 0xFFFFu) * (float)(subblock_ls(h.x, h.y, s) - 32));
             if (kDebug) sL[s][r] = subblock_ls(h.x, h.y, s) - 32;
         }
         // 2. activations: 64 tokens x 16 chunks of 16 codes, four per thread
@@ -146,32 +188,35 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const uint8_t* __r
             const int p = tid + 256 * it;
             const int r = p >> 3, s = p & 7;
             const int64_t m = (m0 + r < M) ? m0 + r : M - 1;
-            sB[s][r] = half_bits_to_float(ads[m * nb + kb * 8 + s] & 0xFFFFu);
+            sB[s][r] = bf16_pair(half_bits_to_float(ads[m * nb + kb * 8 + s] & 0xFFFFu));
         }
         __syncthreads();
 
-        // 3. one MFMA per sub-block, fp32 scale epilogue (the bf16 scale tile of
-        //    the 128x128 kernel measured 5-10 % slower in this one)
+        // 3. one int8 MFMA per sub-block; the scale tiles of two sub-blocks
+        //    from two bf16 MFMAs (scale_outer2), exactly as in the 128x128
+        //    kernel, so that both kernels give bit-identical outputs and the
+        //    tile choice never changes a result
         const int ra = 32 * wn + (lane & 31);
         const int rb = 32 * wm + (lane & 31);
-#pragma unroll 2
-        for (int s = 0; s < 8; ++s) {
-            const int ch = 2 * s + (lane >> 5);
-            const v4i a = *reinterpret_cast<const v4i*>(sW + lds_swz(ra, ch));
-            const v4i b = *reinterpret_cast<const v4i*>(sX + lds_swz(rb, ch));
-            v4f sa[4];
+        const uint32_t bsel = (lane >> 5) ? 0x03020302u : 0x01000100u;
+#pragma unroll 1
+        for (int s = 0; s < 8; s += 2) {
+            v16f sc[2];
+            scale_outer2(*reinterpret_cast<const v2u*>(&sA[s >> 1][ra][0]), sB[s][rb], sB[s + 1][rb], bsel, sc[0], sc[1]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                sa[j] = *reinterpret_cast<const v4f*>(&sA[s][32 * wn + 8 * j + 4 * (lane >> 5)]);
-            const float bx = sB[s][rb];
-            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
+            for (int u = 0; u < 2; ++u) {
+                const int ch = 2 * (s + u) + (lane >> 5);
+                const v4i a = *reinterpret_cast<const v4i*>(sW + lds_swz(ra, ch));
+                const v4i b = *reinterpret_cast<const v4i*>(sX + lds_swz(rb, ch));
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int i = 32 * wn + mfma_c_row(e, lane);
-                acc[e] += (sa[e >> 2][e & 3] * bx) * (float)c[e];
-                if (kDebug) {
-                    const int64_t n = n0 + i, m = m0 + rb;
-                    if (n < N && m < M) dbg[(m * N + n) * nb + kb * 8 + s] = c[e] * sL[s][i];
+                for (int e = 0; e < 16; ++e) {
+                    const int i = 32 * wn + mfma_c_row(e, lane);
+                    acc[e] += sc[u][e] * (float)c[e];
+                    if (kDebug) {
+                        const int64_t n = n0 + i, m = m0 + rb;
+                        if (n < N && m < M) dbg[(m * N + n) * nb + kb * 8 + s + u] = c[e] * sL[s + u][i];
+                    }
                 }
             }
         }
@@ -218,12 +263,10 @@ struct GemmPref {
     uint32_t ds;
 };
 
-template <bool kDebug>
-__global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t* __restrict__ W,
-                                                                   const int8_t* __restrict__ aqs,
-                                                                   const uint32_t* __restrict__ ads,
-                                                                   float* __restrict__ Y, int64_t K, int64_t N,
-                                                                   int64_t M, int64_t ldy_m, int64_t ldy_n,
+template <bool kDebug, bool kGroup>
+__global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const GemmGroup grp, const int8_t* __restrict__ aqs,
+                                                                   const uint32_t* __restrict__ ads, int64_t K,
+                                                                   int64_t M, int64_t ldy_n,
                                                                    int32_t* __restrict__ dbg) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int kStage = kDebug ? G2_STAGE_DBG : G2_STAGE;
@@ -231,7 +274,12 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const uint8_t
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wn = wave & 3, wm = wave >> 2;
-    const int64_t n0 = (int64_t)blockIdx.x * G2_BN;
+    const uint8_t* W;
+    float* Y;
+    int64_t N, ldy_m;
+    int tile0;
+    gemm_select<kGroup>(grp, W, Y, N, ldy_m, tile0);
+    const int64_t n0 = (int64_t)((int)blockIdx.x - tile0) * G2_BN;
     const int64_t m0 = (int64_t)blockIdx.y * G2_BM;
     const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
 
@@ -363,10 +411,11 @@ static int gemm_cu_count() {
     return cached[dev];
 }
 
-// The 128x128 kernel runs one workgroup per CU and is ~1.2x faster per tile;
-// the 64x64 kernel (four per CU) wins when big tiles leave CUs idle: fewer
-// tiles than ~9/16 of the CUs, or a last round that is mostly empty
-// (thresholds from measurements on the 27B-class shapes at M = 512 / 2048).
+// The 128x128 kernel runs one workgroup per CU and is faster per tile; the
+// 64x64 kernel (four per CU) wins when big tiles would leave many CUs idle:
+// fewer tiles than ~9/16 of the CUs (k/v-sized matrices).  Both give
+// bit-identical outputs, so this choice is a speed choice only (thresholds
+// from measurements on the 27B-class shapes at M = 512 / 2048).
 static bool use_big_tiles(int64_t N, int64_t M, int64_t K) {
     // the 128x128 kernel addresses a tile's rows and tokens with 32-bit offsets
     if ((int64_t)G2_BN * (K / QK_K) * BLOCK_BYTES >= (1ll << 32) || (int64_t)G2_BM * K >= (1ll << 32)) return false;
@@ -374,46 +423,72 @@ static bool use_big_tiles(int64_t N, int64_t M, int64_t K) {
     if (k == 0 || k == 1) return k == 1;
     const int64_t cus = gemm_cu_count();
     const int64_t tiles = ((N + G2_BN - 1) / G2_BN) * ((M + G2_BM - 1) / G2_BM);
-    if (tiles < cus * 9 / 16) return false;
-    const int64_t rounds = tiles / cus, rest = tiles % cus;
-    return !(rounds >= 1 && rounds < 4 && rest > 0 && rest <= cus / 4);
+    return tiles >= cus * 9 / 16;
+}
+
+template <bool kDebug, bool kGroup>
+static hipError_t launch_gemm_kernel(bool big, const GemmGroup& grp, int64_t gx, const int8_t* aqs, const uint32_t* ads,
+                                     int64_t K, int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    const int64_t gy = (M + (big ? G2_BM : GEMM_BM) - 1) / (big ? G2_BM : GEMM_BM);
+    if (gx > 0x7FFFFFFF || gy > 65535) return hipErrorInvalidConfiguration;
+    if (big) {
+        static const bool attrs = []() {
+            // two stages exceed the default dynamic-LDS cap; gfx950 has 160 KB per CU
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_iq4xs_db_kernel<kDebug, kGroup>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      2 * (kDebug ? G2_STAGE_DBG : G2_STAGE));
+            return true;
+        }();
+        (void)attrs;
+        hipLaunchKernelGGL((gemm_iq4xs_db_kernel<kDebug, kGroup>), dim3((unsigned)gx, (unsigned)gy), dim3(G2_THREADS),
+                           2 * (size_t)(kDebug ? G2_STAGE_DBG : G2_STAGE), stream, grp, aqs, ads, K, M, ldy_n, dbg);
+    } else {
+        hipLaunchKernelGGL((gemm_iq4xs_mfma_kernel<kDebug, kGroup>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
+                           stream, grp, aqs, ads, K, M, ldy_n, dbg);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     clear_launch_error();
-    if (use_big_tiles(N, M, K)) {
-        const int64_t gx = (N + G2_BN - 1) / G2_BN;
-        const int64_t gy = (M + G2_BM - 1) / G2_BM;
-        if (gx > 0x7FFFFFFF || gy > 65535) return hipErrorInvalidConfiguration;
-        const size_t lds = 2 * (size_t)(dbg ? G2_STAGE_DBG : G2_STAGE);
-        static const bool attrs = []() {
-            // two stages exceed the default dynamic-LDS cap; gfx950 has 160 KB per CU
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_iq4xs_db_kernel<false>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 2 * G2_STAGE);
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_iq4xs_db_kernel<true>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 2 * G2_STAGE_DBG);
-            return true;
-        }();
-        (void)attrs;
-        if (dbg)
-            hipLaunchKernelGGL(gemm_iq4xs_db_kernel<true>, dim3((unsigned)gx, (unsigned)gy), dim3(G2_THREADS), lds,
-                               stream, W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg);
-        else
-            hipLaunchKernelGGL(gemm_iq4xs_db_kernel<false>, dim3((unsigned)gx, (unsigned)gy), dim3(G2_THREADS), lds,
-                               stream, W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg);
-        return hipGetLastError();
+    const bool big = use_big_tiles(N, M, K);
+    GemmGroup grp{};
+    grp.W[0] = W;
+    grp.Y[0] = Y;
+    grp.N[0] = N;
+    grp.ldy_m[0] = ldy_m;
+    const int64_t gx = (N + (big ? G2_BN : GEMM_BN) - 1) / (big ? G2_BN : GEMM_BN);
+    if (gx > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    grp.tile_end[0] = (int)gx;
+    return dbg ? launch_gemm_kernel<true, false>(big, grp, gx, aqs, ads, K, M, ldy_n, dbg, stream)
+               : launch_gemm_kernel<false, false>(big, grp, gx, aqs, ads, K, M, ldy_n, dbg, stream);
+}
+
+// One launch for `count` matrices sharing K and the activations: the tile
+// size is chosen for the summed rows, so the small matrices fill CUs that
+// the big ones' last round leaves idle.
+hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N, const int8_t* aqs,
+                             const uint32_t* ads, int64_t K, int64_t M, bool layout_mk, hipStream_t stream) {
+    clear_launch_error();
+    if (count < 1 || count > GEMV_GROUP_MAX) return hipErrorInvalidValue;
+    int64_t n_sum = 0;
+    for (int i = 0; i < count; ++i) n_sum += N[i];
+    const bool big = use_big_tiles(n_sum, M, K);
+    const int bn = big ? G2_BN : GEMM_BN;
+    GemmGroup grp{};
+    int64_t tiles = 0;
+    for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
+        const int j = i < count ? i : count - 1;  // unused entries repeat the last matrix, past every tile
+        if (i < count) tiles += (N[j] + bn - 1) / bn;
+        if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        grp.W[i] = W[j];
+        grp.Y[i] = Y[j];
+        grp.N[i] = N[j];
+        grp.ldy_m[i] = layout_mk ? N[j] : 1;
+        grp.tile_end[i] = (int)tiles;
     }
-    const int64_t gx = (N + GEMM_BN - 1) / GEMM_BN;
-    const int64_t gy = (M + GEMM_BM - 1) / GEMM_BM;
-    if (gx > 0x7FFFFFFF || gy > 65535) return hipErrorInvalidConfiguration;
-    if (dbg)
-        hipLaunchKernelGGL(gemm_iq4xs_mfma_kernel<true>, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, stream, W,
-                           aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg);
-    else
-        hipLaunchKernelGGL(gemm_iq4xs_mfma_kernel<false>, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, stream, W,
-                           aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg);
-    return hipGetLastError();
+    return launch_gemm_kernel<false, true>(big, grp, tiles, aqs, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
 }
 
 __global__ __launch_bounds__(64) void probe_mfma_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,

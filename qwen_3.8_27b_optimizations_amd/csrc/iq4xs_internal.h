@@ -56,6 +56,11 @@ hipError_t launch_gemv_fused(const uint8_t* W, const float* X, int64_t sc, int64
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
 
+// Y[i] = W[i] x for i < count <= GEMV_GROUP_MAX on the int8 MFMA path, one
+// launch; Y[i] is [M][N[i]] (layout_mk) or [N[i]][M].
+hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N, const int8_t* aqs,
+                             const uint32_t* ads, int64_t K, int64_t M, bool layout_mk, hipStream_t stream);
+
 // One v_mfma_i32_32x32x32_i8 on A[32][32], B[32][32] (k-contiguous rows) ->
 // C[32][32] = A B^T, through the operand layouts the GEMM uses.
 hipError_t launch_probe_mfma(const int8_t* A, const int8_t* B, int32_t* C, hipStream_t stream);

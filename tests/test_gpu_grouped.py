@@ -1,8 +1,10 @@
 """GPU parity of iq4xs_mul_mat_q8_1_group: several matrices against one
 quantised activation set in one launch.  Every output must be bit-identical
 to iq4xs_mul_mat_q8_1 on its own matrix (itself held to the oracle in
-test_gpu_parity.py), and one small case is checked against the oracle
-directly."""
+test_gpu_parity.py) -- including GEMM groups whose tile size differs from
+the single call's, which holds because both GEMM kernels compute each output
+in the same order with the same scale tiles -- and one small case is
+checked against the oracle directly."""
 import numpy as np
 import pytest
 
@@ -27,7 +29,10 @@ GROUP_CASES = [  # K, Ns, M, layout
     (5120, (8192, 1024, 1024), 6, LAYOUT_KM),
     (8192, (5120,), 2, LAYOUT_KM),
     (1024, (40, 33, 9), 2, LAYOUT_MK),            # K < 2048: one launch per matrix
-    (2048, (300, 64), 20, LAYOUT_MK),             # M > 8: the GEMM per matrix
+    (2048, (300, 64), 20, LAYOUT_MK),             # M > 8: one GEMM launch
+    (5120, (8192, 1024, 1024), 512, LAYOUT_MK),   # q alone takes 128x128 tiles, the group 64x64 ones
+    (5120, (17408, 17408), 512, LAYOUT_KM),       # gate/up: 64x64 alone, 128x128 as a group
+    (8192, (130, 4000, 64), 200, LAYOUT_MK),      # ragged tiles in every matrix
 ]
 
 
