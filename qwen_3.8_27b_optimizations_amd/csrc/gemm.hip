@@ -12,13 +12,15 @@
 // Both are VALU-issue bound.  Every output needs its own scale per sub-block,
 // d_w[n] * d_x[m], so the epilogue costs VALU work per output and sub-block
 // against 1/16 of a 32x32x32 int8 MFMA per lane.  The scale tile is formed by
-// a bf16 MFMA from exact hi/lo splits of the two scales (scale_outer), which
+// a bf16 MFMA from exact hi/lo splits of the two scales (scale_outer2), which
 // leaves 2 VALU ops per output and sub-block (convert, fused add) instead of
 // 3 and removes the per-lane row-scale LDS reads: in the 128x128 kernel 8-20 %
 // faster than the multiply version.  The 64x64 kernel measured 3-5 % slower
 // with it than with the multiplies, but uses it too: both kernels then give
 // bit-identical outputs, so the tile choice (which depends on the shape, and
-// for grouped launches on the group) never changes a result.  Measured on the 128x128 kernel before that: removing the
+// for grouped launches on the group) never changes a result.
+//
+// Measured on the 128x128 kernel with the multiply epilogue: removing the
 // int8 MFMA changed little and every VALU op removed showed up in full; an
 // f32 MFMA (32x32x2) for the same outer product cost as much as the 16
 // multiplies; keeping (ls - 32) as int8 with d_w applied once per super-block
