@@ -265,7 +265,11 @@ def test_fused_rejects_oversized_activations(pkg, dev):
 
 
 GEMM_CASES = [(256, 64, 64), (256, 1, 1), (512, 100, 20), (768, 130, 65), (1024, 64, 128),
-              (2048, 200, 100), (512, 64, 512), (256, 300, 9)]
+              (2048, 200, 100), (512, 64, 512), (256, 300, 9),
+              # grids of >= 144 tiles of 128x128 take the double-buffered 128x128 kernel
+              # (its debug instantiation included): one super-block per row; then an odd
+              # super-block count with ragged rows and tokens
+              (256, 128 * 148, 64), (768, 128 * 145 + 33, 33)]
 
 
 @pytest.mark.parametrize("K,N,M", GEMM_CASES)
