@@ -864,15 +864,14 @@ static hipError_t launch_flat_depth(const uint8_t* W, const int8_t* aqs, const u
 }
 
 // Planar columns that go to the matrix-core GEMV: its cost per weight byte
-// does not grow with the columns, the dot4 kernels' does.  Measured per
-// projection shape (K 5120-17408): from 5 columns on it wins every shape with
-// N >= 2048; at 4 the two trade shapes and tie on a layer (graph-replayed
-// decode set: dot4 ahead); below that, and for narrow matrices (k/v,
-// N = 1024: too few 32-row blocks to fill the chip), the dot4 kernels are
-// faster.  Grouped launches use the same rule per matrix, so their outputs
-// match single calls bit for bit.
+// does not grow with the columns, the dot4 kernels' does.  Measured on the
+// graph-replayed decode set (K 5120-17408): from 4 columns on it wins on a
+// layer (bs = 4: 2.10 against 2.01 TB/s); below that, and for narrow matrices
+// (k/v, N = 1024: too few 32-row blocks to fill the chip), the dot4 kernels
+// are faster.  Grouped launches use the same rule per matrix, so their
+// outputs match single calls bit for bit.
 static bool use_gemv_mfma(int64_t N, int64_t M) {
-    static const int min_cols = tuning_knob("IQ4XS_GEMV_MFMA_MIN_COLS", 5, 1, 9);
+    static const int min_cols = tuning_knob("IQ4XS_GEMV_MFMA_MIN_COLS", 4, 1, 9);
     return M >= min_cols && N >= 2048;
 }
 

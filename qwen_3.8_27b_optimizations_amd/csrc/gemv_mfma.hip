@@ -40,10 +40,17 @@ constexpr int GM_LDS_MAX = 160 * 1024;
 constexpr int GM_AROW = 272;  // LDS row of one token's 256 codes, padded (bank spread)
 constexpr int GM_WROW = 144;  // LDS row of one weight row's 128 qs bytes, padded
 constexpr int GM_WAVE_LDS = 32 * GM_WROW + 8 * GM_AROW;  // per-wave staging bytes
+// Register ring of weight super-blocks per wave (one in flight while one is
+// computed); the activations, read by every workgroup and so L2-resident,
+// have a ring of their own, also one super-block ahead.  Depths 3 and 4
+// measured slower (more VGPRs, no better overlap).
+constexpr int GM_RING = 2;
 
-struct GmPref {
+struct GmW {      // weights of one super-block (from HBM: the deep ring)
     v2u h;       // d, scales_h, scales_l of this lane's row's super-block
     v4i q[4];    // qs chunk (lane % 8) of rows lane/8 + 8i: 8 whole rows per load instruction
+};
+struct GmA {      // activations of one super-block (L2-resident: one ahead)
     v4i a[2];    // 32 of the super-block's activation codes: token lane/8, bytes 32*(lane%8) ..
 };
 
@@ -65,16 +72,20 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     int8_t* sact = reinterpret_cast<int8_t*>(swave + 32 * GM_WROW);  // [8][272] activations
     const int wave = tid >> 6;
     const int r0 = blockIdx.x * 32;
-    const int row = min(r0 + col, N - 1);     // rows past N computed, never stored
-    const uint8_t* wrow = W + (size_t)row * bpr * BLOCK_BYTES;   // this lane's row (header)
-    const uint8_t* wchunk[4];                                      // rows lane/8 + 8i, qs chunk lane%8
+    // Global loads are 32-bit lane offsets from workgroup-uniform bases (a
+    // 32-row block spans 32 * K/256 * 136 bytes), which keeps the load ring
+    // in VGPRs.  Rows past N are clamped: computed, never stored.
+    const uint32_t row_bytes = (uint32_t)bpr * BLOCK_BYTES;
+    const uint8_t* wbase = W + (size_t)r0 * row_bytes;
+    const uint32_t off_h = (uint32_t)min(col, N - 1 - r0) * row_bytes;   // this lane's row (header)
+    uint32_t off_q[4];                                                    // rows lane/8 + 8i, qs chunk lane%8
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        wchunk[i] = W + (size_t)min(r0 + (lane >> 3) + 8 * i, N - 1) * bpr * BLOCK_BYTES + 8 + 16 * (lane & 7);
+        off_q[i] = (uint32_t)min((lane >> 3) + 8 * i, N - 1 - r0) * row_bytes + 8 + 16 * (lane & 7);
     uint8_t* wwrite = sw + (lane >> 3) * GM_WROW + 16 * (lane & 7);
     const uint8_t* wread = sw + col * GM_WROW + 8 * h;
     // this lane's share of a super-block's activations, and its MFMA A row in LDS
-    const int8_t* aload = aqs + (size_t)min(lane >> 3, M - 1) * K + 32 * (lane & 7);
+    const uint32_t off_a = (uint32_t)min(lane >> 3, M - 1) * (uint32_t)K + 32 * (lane & 7);
     int8_t* awrite = sact + (lane >> 3) * GM_AROW + 32 * (lane & 7);
     const int8_t* aread = sact + min(col, M - 1) * GM_AROW + 8 * h;
 
@@ -84,23 +95,27 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     }
 
     const int my_n = wave < bpr ? (bpr - wave + GM_WAVES - 1) / GM_WAVES : 0;
-    auto load = [&](GmPref& p, int kb) {
-        p.h = *reinterpret_cast<const v2u*>(wrow + (size_t)kb * BLOCK_BYTES);
+    auto load_w = [&](GmW& p, int kb) {
+        const uint8_t* wk = wbase + (size_t)kb * BLOCK_BYTES;   // uniform
+        p.h = *reinterpret_cast<const v2u*>(wk + off_h);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p.q[i] = *reinterpret_cast<const v4i_a8*>(wchunk[i] + (size_t)kb * BLOCK_BYTES);
-        p.a[0] = *reinterpret_cast<const v4i*>(aload + (size_t)kb * QK_K);
-        p.a[1] = *reinterpret_cast<const v4i*>(aload + (size_t)kb * QK_K + 16);
+        for (int i = 0; i < 4; ++i) p.q[i] = *reinterpret_cast<const v4i_a8*>(wk + off_q[i]);
+    };
+    auto load_a = [&](GmA& p, int kb) {
+        const int8_t* ak = aqs + (size_t)kb * QK_K;               // uniform
+        p.a[0] = *reinterpret_cast<const v4i*>(ak + off_a);
+        p.a[1] = *reinterpret_cast<const v4i*>(ak + off_a + 16);
     };
 
     float acc[4 * G];
 #pragma unroll
     for (int e = 0; e < 4 * G; ++e) acc[e] = 0.0f;
-    auto compute = [&](const GmPref& p, int kb) {
+    auto compute = [&](const GmW& p, const GmA& pa, int kb) {
         // the wave's own LDS rows: written here, read below by other lanes of
         // the same wave (LDS operations of one wave complete in order; the
         // previous super-block's reads were issued before these writes)
-        *reinterpret_cast<v4i*>(awrite) = p.a[0];
-        *reinterpret_cast<v4i*>(awrite + 16) = p.a[1];
+        *reinterpret_cast<v4i*>(awrite) = pa.a[0];
+        *reinterpret_cast<v4i*>(awrite + 16) = pa.a[1];
 #pragma unroll
         for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(wwrite + 8 * i * GM_WROW) = p.q[i];
         const float dw = half_bits_to_float(p.h.x & 0xFFFFu);
@@ -133,17 +148,28 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
             }
         }
     };
-    // ring of 2 with constant indices (unrolled by its depth); every load is
-    // unconditional (past this wave's last super-block it repeats that one)
-    GmPref buf[2];
-    if (my_n > 0) load(buf[0], wave);
-    __syncthreads();  // column scales staged
-    for (int i0 = 0; i0 < my_n; i0 += 2) {
+    // ring of GM_RING super-blocks with constant indices (unrolled by its
+    // depth); every load is unconditional (past this wave's last super-block
+    // it repeats that one)
+    // the loop is unrolled by 2 * GM_RING so that both rings have constant
+    // indices (registers, not scratch)
+    constexpr int UNR = 2 * GM_RING;
+    GmW wb[GM_RING];
+    GmA ab[2];
+    if (my_n > 0) {
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
+        for (int d = 0; d < GM_RING - 1; ++d) load_w(wb[d], wave + GM_WAVES * min(d, my_n - 1));
+        load_a(ab[0], wave);
+    }
+    __syncthreads();  // column scales staged
+    for (int i0 = 0; i0 < my_n; i0 += UNR) {
+#pragma unroll
+        for (int d = 0; d < UNR; ++d) {
             const int i = i0 + d;
-            load(buf[d ^ 1], wave + GM_WAVES * min(i + 1, my_n - 1));
-            if (i < my_n) compute(buf[d], wave + GM_WAVES * i);
+            if (i0 + d >= my_n && d > 0) break;  // uniform: no loads past the last round's end
+            load_w(wb[(d + GM_RING - 1) % GM_RING], wave + GM_WAVES * min(i + GM_RING - 1, my_n - 1));
+            load_a(ab[(d + 1) % 2], wave + GM_WAVES * min(i + 1, my_n - 1));
+            if (i < my_n) compute(wb[d % GM_RING], ab[d % 2], wave + GM_WAVES * i);
         }
     }
 #pragma unroll
