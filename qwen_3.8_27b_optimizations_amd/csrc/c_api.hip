@@ -73,8 +73,10 @@ hipError_t mul_mat_planar(const uint8_t* W, const void* ws, float* Y, int64_t K,
 // Single-column calls with K up to this bound run the GEMV with the Q8_1
 // quantisation in its prologue (one launch, no workspace).  Every workgroup
 // quantises the whole column, so the prologue grows with K: past this bound
-// (and for M > 1) a separate quantiser launch is cheaper.
-constexpr int64_t FUSED_MAX_K = 6144;
+// (and for M > 1) a separate quantiser launch is cheaper (measured on the
+// decode set with one 16-wave workgroup per CU: 8192 ahead of 6144 and of
+// 17408).
+constexpr int64_t FUSED_MAX_K = 8192;
 
 int64_t fused_max_k() {
     static const int64_t v = []() -> int64_t {

@@ -519,8 +519,8 @@ __global__ __launch_bounds__(64 * FLAT_WAVES) void gemv_flat_kernel(
 
 // ---------------------------------------------------------------- row-tile kernel
 // Many short-lived workgroups, each owning R whole rows (R*bpr a multiple of
-// 8, so the tile is a whole number of 8-super-block steps).  The 8 waves of a
-// workgroup interleave the tile's steps (wave w takes steps w, w+8, ...), so
+// 8, so the tile is a whole number of 8-super-block steps).  The 16 waves of
+// a workgroup interleave the tile's steps (wave w takes steps w, w+16, ...), so
 // at any moment a workgroup reads adjacent 1088-byte steps and the grid as a
 // whole sweeps the matrix -- the order HBM serves best.  A wave streams its
 // steps through a ring of D register buffers (each refilled right after it
@@ -529,7 +529,11 @@ __global__ __launch_bounds__(64 * FLAT_WAVES) void gemv_flat_kernel(
 // sub-block term is summed over the 8 lanes of its super-block (DPP) and
 // parked in LDS; rows are summed at the end, in super-block order, so rows
 // may cross steps and waves freely and the result is deterministic.
-constexpr int TILE_WAVES = 8;
+// 16 waves and one tile per CU (38 VGPRs: 4 waves per SIMD) measured ahead of
+// 8 waves and two tiles per CU: the same waves per CU, but half the
+// workgroups stage (or, fused, quantise) the activations (graph-replayed
+// decode set: fused step +5.5 %, prequantised +1.5 %, bs = 2 +4.5 %).
+constexpr int TILE_WAVES = 16;
 
 // Up to GEMV_GROUP_MAX weight matrices with the same K that read the same
 // activations, run by one launch: matrix g owns tiles [tile_end[g-1],
@@ -779,7 +783,7 @@ static hipError_t launch_flat(const uint8_t* W, const int8_t* aqs, const uint32_
 // sized for about `tiles_per_cu` tiles per CU.
 static int64_t tile_rows(int64_t bpr, int64_t N) {
     const int64_t g = 8 / std::gcd<int64_t, int64_t>(bpr, 8);
-    static const int tiles_per_cu = tuning_knob("IQ4XS_GEMV_TILES_PER_CU", 2, 1, 64);
+    static const int tiles_per_cu = tuning_knob("IQ4XS_GEMV_TILES_PER_CU", 1, 1, 64);
     const int64_t tiles = (int64_t)tiles_per_cu * device_cu_count();
     const int64_t units = (N + g - 1) / g;
     return ((units + tiles - 1) / tiles) * g;

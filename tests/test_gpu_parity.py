@@ -219,7 +219,7 @@ def test_gemv_sums_and_outputs(pkg, orc, dev, K, N, M):
     assert torch.equal(Y, Y2)  # the debug store does not change the arithmetic
 
 
-FUSED_CASES = [(256, 1, 1, LAYOUT_MK), (5120, 333, 1, LAYOUT_MK), (17408, 40, 1, LAYOUT_MK),
+FUSED_CASES = [(256, 1, 1, LAYOUT_MK), (5120, 333, 1, LAYOUT_MK), (8192, 333, 1, LAYOUT_MK), (17408, 40, 1, LAYOUT_MK),
                (768, 9, 2, LAYOUT_KM), (2048, 130, 4, LAYOUT_MK), (5120, 100, 6, LAYOUT_KM),
                (8192, 96, 7, LAYOUT_MK), (5120, 64, 8, LAYOUT_KM)]
 
