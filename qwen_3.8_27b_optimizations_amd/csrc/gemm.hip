@@ -157,6 +157,44 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const GemmGroup gr
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
 
+    // This thread's share of a super-block's global loads, held in registers:
+    // the next super-block is in flight during the current MFMA phase (a lone
+    // workgroup on a CU, as for k/v-sized grids, would otherwise wait one DRAM
+    // round trip per super-block).  Rows / tokens past the end are clamped.
+    struct Pref64 {
+        uint2 h[2];
+        v4i w[2];
+        v4i x[4];
+        uint32_t ds[2];
+    };
+    auto load = [&](Pref64& g, int64_t kb) {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int p = tid + 256 * it;
+            const int r = p >> 3, s = p & 7;
+            const int64_t n = (n0 + r < N) ? n0 + r : N - 1;
+            const uint8_t* blk = W + n * row_bytes + kb * BLOCK_BYTES;
+            g.h[it] = *reinterpret_cast<const uint2*>(blk);
+            g.w[it] = *reinterpret_cast<const v4i_a8*>(blk + 8 + 16 * s);
+        }
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int p = tid + 256 * it;
+            const int r = p >> 4, c = p & 15;
+            const int64_t m = (m0 + r < M) ? m0 + r : M - 1;
+            g.x[it] = *reinterpret_cast<const v4i*>(aqs + m * K + kb * QK_K + 16 * c);
+        }
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int p = tid + 256 * it;
+            const int r = p >> 3, s = p & 7;
+            const int64_t m = (m0 + r < M) ? m0 + r : M - 1;
+            g.ds[it] = ads[m * nb + kb * 8 + s];
+        }
+    };
+    Pref64 g;
+    load(g, 0);
+
     for (int64_t kb = 0; kb < bpr; ++kb) {
         __syncthreads();
         // 1. weights: 64 rows x 8 sub-blocks, two (row, sub-block) pairs per thread
@@ -164,10 +202,8 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const GemmGroup gr
         for (int it = 0; it < 2; ++it) {
             const int p = tid + 256 * it;
             const int r = p >> 3, s = p & 7;
-            const int64_t n = (n0 + r < N) ? n0 + r : N - 1;
-            const uint8_t* blk = W + n * row_bytes + kb * BLOCK_BYTES;
-            const uint2 h = *reinterpret_cast<const uint2*>(blk);
-            const v4i w = *reinterpret_cast<const v4i_a8*>(blk + 8 + 16 * s);
+            const uint2 h = g.h[it];
+            const v4i w = g.w[it];
             uint32_t lo[4], hi[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)w[j], lo[j], hi[j]);
@@ -181,18 +217,16 @@ __global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const GemmGroup gr
         for (int it = 0; it < 4; ++it) {
             const int p = tid + 256 * it;
             const int r = p >> 4, c = p & 15;
-            const int64_t m = (m0 + r < M) ? m0 + r : M - 1;
-            *reinterpret_cast<v4i*>(sX + lds_swz(r, c)) =
-                *reinterpret_cast<const v4i*>(aqs + m * K + kb * QK_K + 16 * c);
+            *reinterpret_cast<v4i*>(sX + lds_swz(r, c)) = g.x[it];
         }
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
             const int p = tid + 256 * it;
             const int r = p >> 3, s = p & 7;
-            const int64_t m = (m0 + r < M) ? m0 + r : M - 1;
-            sB[s][r] = bf16_pair(half_bits_to_float(ads[m * nb + kb * 8 + s] & 0xFFFFu));
+            sB[s][r] = bf16_pair(half_bits_to_float(g.ds[it] & 0xFFFFu));
         }
         __syncthreads();
+        if (kb + 1 < bpr) load(g, kb + 1);  // in flight during the MFMA phase
 
         // 3. one int8 MFMA per sub-block; the scale tiles of two sub-blocks
         //    from two bf16 MFMAs (scale_outer2), exactly as in the 128x128
