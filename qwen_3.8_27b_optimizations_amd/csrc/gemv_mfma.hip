@@ -193,6 +193,10 @@ static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t*
     const size_t lds = ((size_t)(K / QK8_1) * 8 + (size_t)WAVES * 4 * 64) * sizeof(float) +
                        (size_t)WAVES * GM_WAVE_LDS;
     if (lds > GM_LDS_MAX) return hipErrorNotSupported;
+    // the kernel's 32-bit load offsets span one 32-row block and 8 token rows
+    // (the LDS budget above already keeps K far below this)
+    if ((int64_t)32 * (K / QK_K) * BLOCK_BYTES >= ((int64_t)1 << 31) || (int64_t)8 * K >= ((int64_t)1 << 31))
+        return hipErrorNotSupported;
     if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit of a launch
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_mfma_kernel<WAVES, false>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS_MAX);
