@@ -196,7 +196,8 @@ def mul_mat_q8_1(W, ws, K: int, N: int, M: int, layout: int = LAYOUT_MK, path: i
 
 
 def mul_mat_q8_1_group(Ws, ws, K: int, Ns, M: int, layout: int = LAYOUT_MK, outs=None):
-    """[W_i * dequant(ws)] for up to 4 matrices sharing the activations (one GEMV launch for M <= 8)."""
+    """[W_i * dequant(ws)] for up to 4 matrices sharing the activations, in one launch (the GEMV for
+    M <= 8, the GEMM above); each output bit-identical to mul_mat_q8_1 on its own matrix."""
     torch = _torch()
     n = len(Ws)
     if not 1 <= n <= 4 or len(Ns) != n:
