@@ -205,8 +205,9 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
     eps = 1e-6
     P = pkg.PATH_AUTO
 
-    def chain(M: int, grouped: bool = False):
+    def chain(M: int, grouped: bool = False, fused: bool = False):
         h = pkg.synthetic_activations(M * H_DIM, seed=700, device=dev)
+        h_alt = torch.empty_like(h)  # the fused norm writes h into the other buffer (no in-place form)
         bufs = {name: torch.zeros((M, N), device=dev) for name, _, N in SHAPES}
         wsA = torch.empty(L.iq4xs_workspace_bytes(H_DIM, M), dtype=torch.uint8, device=dev)
         wsB = torch.empty(L.iq4xs_workspace_bytes(Q_DIM, M), dtype=torch.uint8, device=dev)
@@ -231,33 +232,46 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
             n, wp, yp, nn = gargs[l][which]
             L.check("iq4xs_mul_mat_q8_1_group", n, wp, yp, nn, ws.data_ptr(), K, M, pkg.LAYOUT_MK, s)
 
+        def rms_group(l, which, X, R, H):
+            n, wp, yp, nn = gargs[l][which]
+            L.check("iq4xs_rms_norm_mul_mat_group", n, wp, yp, nn, X.data_ptr(), R.data_ptr(), H.data_ptr(),
+                    gain.data_ptr(), eps, H_DIM, s)
+
         def run() -> None:
             for l in range(args.model_layers):
                 Wl = weights[l]
-                L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["down_proj"].data_ptr(), h.data_ptr(),
-                        gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
-                if grouped:
-                    mm_group(l, 0, wsA, H_DIM)
+                if fused:  # h + down_prev -> h_alt, norm, q/k/v: one launch
+                    rms_group(l, 0, h, bufs["down_proj"], h_alt)
                 else:
-                    for i in range(3):
-                        mm(Wl[i], wsA, *SHAPES[i])
+                    L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["down_proj"].data_ptr(), h.data_ptr(),
+                            gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
+                    if grouped:
+                        mm_group(l, 0, wsA, H_DIM)
+                    else:
+                        for i in range(3):
+                            mm(Wl[i], wsA, *SHAPES[i])
                 L.check("iq4xs_quantize_q8_1", bufs["q_proj"].data_ptr(), Q_DIM, M, pkg.LAYOUT_MK, wsB.data_ptr(),
                         wsB.numel(), s)
                 mm(Wl[3], wsB, *SHAPES[3])
-                L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["o_proj"].data_ptr(), h.data_ptr(),
-                        gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
-                if grouped:
-                    mm_group(l, 1, wsA, H_DIM)
+                if fused:  # h_alt + o -> h, norm, gate/up: one launch
+                    rms_group(l, 1, h_alt, bufs["o_proj"], h)
                 else:
-                    mm(Wl[4], wsA, *SHAPES[4])
-                    mm(Wl[5], wsA, *SHAPES[5])
+                    L.check("iq4xs_rms_norm_q8_1", h.data_ptr(), bufs["o_proj"].data_ptr(), h.data_ptr(),
+                            gain.data_ptr(), eps, H_DIM, M, wsA.data_ptr(), wsA.numel(), s)
+                    if grouped:
+                        mm_group(l, 1, wsA, H_DIM)
+                    else:
+                        mm(Wl[4], wsA, *SHAPES[4])
+                        mm(Wl[5], wsA, *SHAPES[5])
                 L.check("iq4xs_swiglu_q8_1", bufs["gate_proj"].data_ptr(), bufs["up_proj"].data_ptr(), FF_DIM, M,
                         wsC.data_ptr(), wsC.numel(), s)
                 mm(Wl[6], wsC, *SHAPES[6])
 
         def finite() -> bool:
             torch.cuda.synchronize()
-            return bool(torch.isfinite(h).all()) and all(bool(torch.isfinite(v).all()) for v in bufs.values())
+            hs = [h, h_alt] if fused else [h]
+            return all(bool(torch.isfinite(t).all()) for t in hs) and all(
+                bool(torch.isfinite(v).all()) for v in bufs.values())
 
         return run, finite
 
@@ -281,6 +295,17 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
                           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                           "tokens_per_s_upper_bound": round(1e6 / us, 1), "finite": finite_g(),
                           "note": "same chain; q,k,v and gate,up each one iq4xs_mul_mat_q8_1_group launch"}
+    del run
+    token_f, finite_f = chain(1, fused=True)
+    run, _ = capture(torch, stream, token_f, use_graph)
+    timer(run, 2)
+    us = timer(run, 8) / 8
+    gbs = layer_bytes * args.model_layers / (us * 1e-6) / 1e9
+    out["bs1_rms_fused"] = {"us_per_token": round(us, 1), "GBps": round(gbs, 1),
+                            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                            "tokens_per_s_upper_bound": round(1e6 / us, 1), "finite": finite_f(),
+                            "note": "same chain; each rms norm and the q,k,v / gate,up group after it are one "
+                                    "iq4xs_rms_norm_mul_mat_group launch"}
     del run
     M = 512
     prefill, finite512 = chain(M)

@@ -182,8 +182,7 @@ int iq4xs_quantize_q8_1(const float* X, int64_t K, int64_t M, int layout, void* 
  * planar Q8_1 in ws on the way out (row-major inputs, row m at [m*K]).  They
  * stand for ggml's RMS_NORM + MUL and SWIGLU ahead of the projections
  * (profiled by the reference at benchmarks/profiling/BOTTLENECK-TABLE.md:
- * 24,26,30) and have no kernel counterpart in the reference; survey rank 2
- * of the next steps.  K % 32 == 0.
+ * 24,26,30) and have no kernel counterpart in the reference.  K % 32 == 0.
  *
  * rms norm: h = X + R (R may be NULL), written to H when H is non-NULL
  * (H may be exactly X or R: the in-place residual add); then
@@ -199,6 +198,22 @@ int iq4xs_rms_norm_q8_1(const float* X, const float* R, float* H, const float* g
  * library's own Cody-Waite reduction, <= 1 ulp). */
 int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void* ws, size_t ws_bytes,
                       void* stream);
+
+/* RMS norm fused into a grouped bs=1 GEMV: the same result as
+ * iq4xs_rms_norm_q8_1(X, R, H, gamma, eps, K, 1, ws) followed by
+ * iq4xs_mul_mat_q8_1_group(count, W, Y, N, ws, K, 1, ...) -- Y and H bit for
+ * bit -- in one launch and with no workspace: every workgroup of the GEMV
+ * runs the norm's passes on the row and quantises it into its own LDS, and
+ * workgroup 0 writes H.  For the norm ahead of q/k/v or gate/up at decode.
+ * No counterpart in the reference, which runs RMS_NORM, MUL and each
+ * projection as separate ggml ops.
+ *   - H (may be NULL) must not overlap X or R, and no Y[i] may overlap X, R or H
+ *     (in-place forms are rejected with hipErrorInvalidValue);
+ *   - X, R, H 16-byte aligned; K % 256 == 0, eps >= 0;
+ *   - hipErrorNotSupported for K < 2048 or K > 16384, or when the row does not
+ *     fit the kernel's LDS (K <= ~10000 at typical shapes): use the two calls. */
+int iq4xs_rms_norm_mul_mat_group(int count, const void* const* W, float* const* Y, const int64_t* N, const float* X,
+                                 const float* R, float* H, const float* gamma, float eps, int64_t K, void* stream);
 
 /* Y = W * dequant(ws) from an already quantised workspace; `layout` selects
  * the Y layout; `path` is one of IQ4XS_PATH_*. */

@@ -73,6 +73,7 @@ SIGNATURES = {
     "iq4xs_mul_mat_q8_1_group": (_INT, [_INT, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
     "iq4xs_rms_norm_q8_1": (_INT, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, _P, ctypes.c_size_t, _P]),
     "iq4xs_swiglu_q8_1": (_INT, [_P, _P, _I64, _I64, _P, ctypes.c_size_t, _P]),
+    "iq4xs_rms_norm_mul_mat_group": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, ctypes.c_float, _I64, _P]),
     "iq4xs_q8_1_to_blocks": (_INT, [_P, _P, _I64, _I64, _P]),
     "iq4xs_subblock_sums": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "iq4xs_probe_mfma_i8": (_INT, [_P, _P, _P, _P]),
@@ -174,6 +175,24 @@ def swiglu_q8_1(G, U, K: int, M: int, ws=None):
     ws = workspace(K, M, G.device) if ws is None else ws
     lib().check("iq4xs_swiglu_q8_1", G.data_ptr(), U.data_ptr(), K, M, ws.data_ptr(), ws.numel(), _stream(torch))
     return ws
+
+
+def rms_norm_mul_mat_group(Ws, X, K: int, Ns, residual=None, out_h=None, gamma=None, eps: float = 1e-6, outs=None):
+    """RMS norm of one column (h = X + residual, written to out_h) fused into one grouped bs=1 GEMV:
+    [W_i * Q8_1((h * scale) * gamma)], bit-identical to rms_norm_q8_1 followed by mul_mat_q8_1_group."""
+    torch = _torch()
+    n = len(Ws)
+    if outs is None:
+        outs = [torch.empty(N, dtype=torch.float32, device=X.device) for N in Ns]
+    for W, N in zip(Ws, Ns):
+        _check_weights(W, K, N)
+    wp = (ctypes.c_void_p * n)(*[W.data_ptr() for W in Ws])
+    yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in outs])
+    nn = (ctypes.c_int64 * n)(*Ns)
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    lib().check("iq4xs_rms_norm_mul_mat_group", n, wp, yp, nn, X.data_ptr(), ptr(residual), ptr(out_h), ptr(gamma),
+                eps, K, _stream(torch))
+    return outs
 
 
 def q8_1_blocks(ws, K: int, M: int):

@@ -333,6 +333,25 @@ int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void
     return launch_swiglu_q8_1(G, U, K, M, p.qs, p.ds, as_stream(stream));
 }
 
+int iq4xs_rms_norm_mul_mat_group(int count, const void* const* W, float* const* Y, const int64_t* N, const float* X,
+                                 const float* R, float* H, const float* gamma, float eps, int64_t K, void* stream) {
+    if (count < 1 || count > GEMV_GROUP_MAX || !W || !Y || !N || !X || !valid_k(K) || K >= MAX_DIM)
+        return hipErrorInvalidValue;
+    if (!(eps >= 0.0f) || !aligned16(X) || !aligned16(R) || !aligned16(H)) return hipErrorInvalidValue;
+    // workgroup 0 writes H while the others still read X and R: no aliasing
+    const size_t bytes = (size_t)K * sizeof(float);
+    if (overlaps(H, bytes, X, bytes) || overlaps(H, bytes, R, bytes)) return hipErrorInvalidValue;
+    for (int i = 0; i < count; ++i) {
+        if (!W[i] || !Y[i] || N[i] <= 0 || N[i] >= MAX_DIM) return hipErrorInvalidValue;
+        const size_t yb = (size_t)N[i] * sizeof(float);
+        if (overlaps(Y[i], yb, X, bytes) || overlaps(Y[i], yb, R, bytes) || overlaps(Y[i], yb, H, bytes))
+            return hipErrorInvalidValue;
+    }
+    const uint8_t* Wb[GEMV_GROUP_MAX];
+    for (int i = 0; i < count; ++i) Wb[i] = static_cast<const uint8_t*>(W[i]);
+    return launch_gemv_rms_group(count, Wb, Y, N, X, R, H, gamma, eps, K, as_stream(stream));
+}
+
 int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, void* stream) {
     if (!ws || !blocks || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
     const Planar p = planar_view(ws, K, M);

@@ -31,6 +31,7 @@
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 #include "q8_1_block.h"
+#include "rms_device.h"
 
 namespace iq4xs {
 
@@ -547,11 +548,25 @@ struct GemvGroup {
     int tile_end[GEMV_GROUP_MAX];
 };
 
-template <int C, int D, bool kDebug, bool kFuse, bool kGroup>
+// Arguments of the fused RMS-norm prologue (kRms): h = X (+ R), written to H
+// by workgroup 0 only; the Q8_1 codes of (h * scale) * gamma go to LDS.
+struct RmsArgs {
+    const float* R;
+    float* H;
+    const float* gamma;
+    float eps;
+};
+
+// kRms: 0 = none; bit 0 = the RMS-norm prologue (C == 1), bit 1 = with a
+// residual R, bit 2 = with a gain gamma.
+template <int C, int D, bool kDebug, bool kFuse, bool kGroup, int kRms = 0>
 __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const GemvGroup grp, const int8_t* __restrict__ aqs, const uint32_t* __restrict__ ads,
     const float* __restrict__ X, int64_t sc, int64_t sk, int K, int64_t ldy_n, int rows_per_wg,
-    int32_t* __restrict__ dbg) {
+    int32_t* __restrict__ dbg, const RmsArgs rms) {
+    constexpr bool kRmsOn = (kRms & 1) != 0, kRmsRes = (kRms & 2) != 0, kRmsGain = (kRms & 4) != 0;
+    static_assert(!kRmsOn || (C == 1 && !kFuse && RMS_THREADS == 64 * TILE_WAVES),
+                  "the RMS prologue runs the producer's own 1024-thread reduction on one column");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint8_t* __restrict__ W = grp.W[0];
     float* __restrict__ Y = grp.Y[0];
@@ -613,6 +628,8 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const bool split = kFuse && C == 1 && tasks <= 4 * nthreads;
     FusedRegs fx;
     if (split) fused_load(fx, X, sk, tasks, tid, nthreads);
+    RmsBatch rb;  // the RMS prologue's pass-1 loads (one batch: K <= RMS_ONE_BATCH_K), also ahead of the prefetch
+    if (kRmsOn) rms_load<kRmsRes>(rb, X, rms.R, 4 * tid, K);
     // Every weight load is unconditional (steps past this wave's last one
     // repeat it), so the wait counts are compile-time exact.
     StepRegs buf[D];
@@ -626,7 +643,44 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     while (u >= bpr) u -= bpr;
     int sb_stride = TILE_WAVES * 8;
     while (sb_stride >= bpr) sb_stride -= bpr;
-    if (split) {
+    if constexpr (kRmsOn) {
+        // the producer's passes (rms_device.h), with h staged in LDS after the
+        // partials and the codes written straight to the GEMV's LDS operand
+        __shared__ double rms_part[RMS_WAVES];
+        const size_t h_off = ((size_t)K + (size_t)nb * 4 + (size_t)rows_per_wg * bpr * 4 + 15) & ~(size_t)15;
+        float* shh = reinterpret_cast<float*>(lds + h_off);
+        const double acc = rms_accumulate<kRmsRes, true>(rb, blockIdx.x == 0 ? rms.H : nullptr, shh, 4 * tid, K, 0.0);
+        const int j = q8_lane_elem(tid & 7);
+        constexpr int STEP = RMS_THREADS / 8;
+        const int b0 = tid >> 3;
+        float gcur[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (kRmsGain) {
+            const int e = (b0 < nb ? b0 : nb - 1) * QK8_1 + j;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gcur[i] = rms.gamma[e + 8 * i];
+        }
+        const float scale = rms_scale(rms_reduce(acc, rms_part, tid), K, rms.eps);
+        for (int b = b0; b < nb; b += STEP) {  // uniform per 8-lane group
+            const int e = b * QK8_1 + j;
+            float gnext[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (kRmsGain) {
+                const int bn = b + STEP < nb ? b + STEP : nb - 1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gnext[i] = rms.gamma[bn * QK8_1 + j + 8 * i];
+            }
+            float y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[i] = rms_y<kRmsGain>(shh[e + 8 * i], scale, gcur[i]);
+            const Q8Block8 q = quantize_block8(y[0], y[1], y[2], y[3]);
+            sq[e] = (int8_t)q.q0;
+            sq[e + 8] = (int8_t)q.q1;
+            sq[e + 16] = (int8_t)q.q2;
+            sq[e + 24] = (int8_t)q.q3;
+            if (j == 0) sdx[b] = half_bits_to_float(q.ds & 0xFFFFu);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gcur[i] = gnext[i];
+        }
+    } else if (split) {
         fused_store(fx, sq, sdx, tasks, tid, nthreads);
     } else if (kFuse) {
         quantize_to_lds<C>(X, sc, sk, K, sq, sdx, tid, nthreads);
@@ -818,11 +872,11 @@ static hipError_t launch_tile_d(const TileMat* mats, int count, const int8_t* aq
     const dim3 grid((unsigned)wgs), block(64 * TILE_WAVES);
 #define IQ4XS_LAUNCH_TILE(DBG, FUSE)                                                                              \
     hipLaunchKernelGGL((gemv_tile_kernel<C, D, DBG, FUSE, false>), grid, block, lds, stream, grp, aqs, ads, X, sc, \
-                       sk, (int)K, ldy_n, (int)R, dbg)
+                       sk, (int)K, ldy_n, (int)R, dbg, RmsArgs{})
     if (count > 1) {
         if (X != nullptr || dbg != nullptr) return hipErrorNotSupported;  // grouped: planar activations only
         hipLaunchKernelGGL((gemv_tile_kernel<C, D, false, false, true>), grid, block, lds, stream, grp, aqs, ads, X,
-                           sc, sk, (int)K, ldy_n, (int)R, dbg);
+                           sc, sk, (int)K, ldy_n, (int)R, dbg, RmsArgs{});
     } else if (X != nullptr) {
         if (dbg) IQ4XS_LAUNCH_TILE(true, true); else IQ4XS_LAUNCH_TILE(false, true);
     } else {
@@ -962,6 +1016,54 @@ hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y
         if (err != hipSuccess) return err;
     }
     return hipSuccess;
+}
+
+template <int MODE>
+static void launch_rms_tile(dim3 grid, dim3 block, size_t lds, hipStream_t stream, const GemvGroup& grp,
+                            const float* X, int64_t K, int64_t R, const RmsArgs& a) {
+    hipLaunchKernelGGL((gemv_tile_kernel<1, 2, false, false, true, MODE>), grid, block, lds, stream, grp, nullptr,
+                       nullptr, X, 0, 1, (int)K, 1, (int)R, nullptr, a);
+}
+
+// RMS norm of one column fused into the prologue of a grouped bs=1 GEMV: every
+// workgroup runs the producer's passes on the whole row (h staged in LDS, the
+// Q8_1 codes straight into the GEMV's operand), workgroup 0 writes H.  The
+// codes, and so every output, are those of iq4xs_rms_norm_q8_1 followed by the
+// grouped GEMV.  hipErrorNotSupported past one pass-1 batch (K > 16384), below
+// the tile kernel's K >= 2048, or when the LDS does not fit.
+hipError_t launch_gemv_rms_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
+                                 const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                                 hipStream_t stream) {
+    clear_launch_error();
+    const int64_t bpr = K / QK_K, nb = K / QK8_1;
+    if (count < 1 || count > GEMV_GROUP_MAX || bpr < 8 || K > RMS_ONE_BATCH_K) return hipErrorNotSupported;
+    int64_t rows = 0;
+    for (int i = 0; i < count; ++i) rows += N[i];
+    const int64_t Rr = tile_rows(bpr, rows);
+    if (Rr * bpr * BLOCK_BYTES >= ((int64_t)1 << 31) || rows >= ((int64_t)1 << 30)) return hipErrorNotSupported;
+    GemvGroup grp{};
+    int64_t wgs = 0;
+    for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
+        const int k = i < count ? i : count - 1;
+        if (i < count) wgs += (N[k] + Rr - 1) / Rr;
+        grp.W[i] = W[k];
+        grp.Y[i] = Y[k];
+        grp.ldy_m[i] = N[k];
+        grp.N[i] = (int)N[k];
+        grp.tile_end[i] = (int)(wgs < 0x7FFFFFFF ? wgs : 0x7FFFFFFF);
+    }
+    const size_t h_off = ((size_t)K + (size_t)nb * 4 + (size_t)Rr * bpr * 4 + 15) & ~(size_t)15;
+    const size_t lds = h_off + (size_t)K * 4;
+    if (lds > GEMV_LDS_BUDGET || wgs > 0x7FFFFFFF) return hipErrorNotSupported;
+    const dim3 grid((unsigned)wgs), block(64 * TILE_WAVES);
+    const RmsArgs a{R, H, gamma, eps};
+    switch ((R ? 2 : 0) | (gamma ? 4 : 0)) {
+        case 0: launch_rms_tile<1>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+        case 2: launch_rms_tile<3>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+        case 4: launch_rms_tile<5>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+        default: launch_rms_tile<7>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,

@@ -52,6 +52,13 @@ hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y
 hipError_t launch_gemv_fused(const uint8_t* W, const float* X, int64_t sc, int64_t sk, float* Y, int64_t K, int64_t N,
                              int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
 
+// RMS norm of one column (h = X (+ R), written to H when non-null; y = (h *
+// scale) * gamma) fused into a grouped bs=1 GEMV over its Q8_1 codes;
+// hipErrorNotSupported for shapes the fused prologue does not take.
+hipError_t launch_gemv_rms_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
+                                 const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                                 hipStream_t stream);
+
 // Same contract on the int8 MFMA path (any M >= 1).
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                        int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);

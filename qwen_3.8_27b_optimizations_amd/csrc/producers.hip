@@ -25,6 +25,7 @@
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 #include "q8_1_block.h"
+#include "rms_device.h"
 
 #pragma clang fp contract(off)
 
@@ -80,16 +81,13 @@ __global__ __launch_bounds__(256) void swiglu_q8_1_kernel(const float* __restric
     store_block8(quantize_block8(y[0], y[1], y[2], y[3]), qs + e, ds + blk, j);
 }
 
-// One work-group of RMS_THREADS threads (16 waves) per row.  Pass 1 forms h
-// (writing it to H when asked) and reduces its sum of squares; pass 2
-// quantises y block by block, 8 lanes per block.  A thread's loads for up to
-// RMS_BATCH vectors are issued before any of its stores, so the row streams
-// in one or two round trips even though H may alias X or R.  With kLds
-// (K <= RMS_LDS_MAX) h is staged in LDS for pass 2; otherwise pass 2 re-reads
-// it (from H, or recomputes x + r).
-constexpr int RMS_THREADS = 1024;
-constexpr int RMS_WAVES = RMS_THREADS / 64;
-constexpr int RMS_BATCH = 4;
+// One work-group of RMS_THREADS threads (16 waves) per row, with the
+// arithmetic of rms_device.h.  Pass 1 forms h (writing it to H when asked)
+// and reduces its sum of squares; pass 2 quantises y block by block, 8 lanes
+// per block.  A thread's loads for up to RMS_BATCH vectors are issued before
+// any of its stores, so the row streams in one or two round trips even though
+// H may alias X or R.  With kLds (K <= RMS_LDS_MAX) h is staged in LDS for
+// pass 2; otherwise pass 2 re-reads it (from H, or recomputes x + r).
 constexpr int64_t RMS_LDS_MAX = 32768;  // up to 128 KB of LDS per row
 
 template <bool kLds, bool kRes, bool kGain>
@@ -107,29 +105,9 @@ __global__ __launch_bounds__(RMS_THREADS) void rms_norm_q8_1_kernel(const float*
 
     double acc = 0.0;
     for (int64_t k0 = 4 * t; k0 < K; k0 += 4 * RMS_THREADS * RMS_BATCH) {
-        // every load unconditional (index clamped into the row), all issued
-        // before the first use
-        v4f v[RMS_BATCH], w[RMS_BATCH];
-#pragma unroll
-        for (int u = 0; u < RMS_BATCH; ++u) {
-            const int64_t k = k0 + 4 * RMS_THREADS * u < K ? k0 + 4 * RMS_THREADS * u : K - 4;
-            v[u] = *reinterpret_cast<const v4f*>(x + k);
-            if (kRes) w[u] = *reinterpret_cast<const v4f*>(r + k);
-        }
-#pragma unroll
-        for (int u = 0; u < RMS_BATCH; ++u) {
-            const int64_t k = k0 + 4 * RMS_THREADS * u;
-            if (k < K) {
-                if (kRes) v[u] = v4f{v[u].x + w[u].x, v[u].y + w[u].y, v[u].z + w[u].z, v[u].w + w[u].w};
-                if (h) *reinterpret_cast<v4f*>(h + k) = v[u];
-                if (kLds) *reinterpret_cast<v4f*>(sh + k) = v[u];
-                const float s0 = v[u].x * v[u].x, s1 = v[u].y * v[u].y, s2 = v[u].z * v[u].z, s3 = v[u].w * v[u].w;
-                acc = acc + (double)s0;
-                acc = acc + (double)s1;
-                acc = acc + (double)s2;
-                acc = acc + (double)s3;
-            }
-        }
+        RmsBatch b;
+        rms_load<kRes>(b, x, r, k0, K);
+        acc = rms_accumulate<kRes, kLds>(b, h, sh, k0, K, acc);
     }
     // pass 2's gains: this thread's first block is fetched now (clamped, so
     // unconditional), each next one an iteration ahead
@@ -143,21 +121,7 @@ __global__ __launch_bounds__(RMS_THREADS) void rms_norm_q8_1_kernel(const float*
 #pragma unroll
         for (int i = 0; i < 4; ++i) gcur[i] = gamma[e + 8 * i];
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc = acc + __shfl_xor(acc, o, 64);
-    if ((t & 63) == 0) part[t >> 6] = acc;
-    __syncthreads();  // also orders this group's H and LDS stores before pass 2 reads them
-    double p[RMS_WAVES];
-#pragma unroll
-    for (int i = 0; i < RMS_WAVES; ++i) p[i] = part[i];
-#pragma unroll
-    for (int n = RMS_WAVES / 2; n > 0; n >>= 1) {
-#pragma unroll
-        for (int i = 0; i < n; ++i) p[i] = p[2 * i] + p[2 * i + 1];
-    }
-    const double ss = p[0];
-    const float mean = (float)(ss / (double)K);
-    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
+    const float scale = rms_scale(rms_reduce(acc, part, t), K, eps);
 
     const float* src = kLds ? sh : (h ? h : x);
     for (int64_t b = b0; b < nb; b += STEP) {  // uniform per 8-lane group
@@ -173,8 +137,7 @@ __global__ __launch_bounds__(RMS_THREADS) void rms_norm_q8_1_kernel(const float*
         for (int i = 0; i < 4; ++i) {
             float v = src[e + 8 * i];
             if (!kLds && !h && kRes) v = v + r[e + 8 * i];
-            const float sc = v * scale;
-            y[i] = kGain ? sc * gcur[i] : sc;
+            y[i] = rms_y<kGain>(v, scale, kGain ? gcur[i] : 0.0f);
         }
         store_block8(quantize_block8(y[0], y[1], y[2], y[3]), qs + m * K + e, ds + m * nb + b, j);
         if (kGain) {

@@ -1,0 +1,86 @@
+"""iq4xs_rms_norm_mul_mat_group: the RMS norm of one column fused into the
+prologue of a grouped bs=1 GEMV.  Its outputs (every Y[i], and H) must be
+bit-identical to iq4xs_rms_norm_q8_1 followed by iq4xs_mul_mat_q8_1_group,
+both held to the oracle elsewhere (test_gpu_producers.py, test_gpu_grouped.py);
+the fused kernel runs the producer's own reduction order (rms_device.h)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    torch.cuda.set_device(0)
+    return torch.device("cuda:0")
+
+
+def bits(t):
+    return t.contiguous().cpu().numpy().view(np.uint32)
+
+
+CASES = [  # K, Ns, residual, gain, write H
+    (5120, (8192, 1024, 1024), True, True, True),    # q, k, v after the attention norm
+    (5120, (17408, 17408), True, True, True),        # gate, up after the FFN norm
+    (5120, (7, 130, 1), True, True, False),          # ragged last tiles, N = 1
+    (2048, (300, 64), False, True, True),            # smallest K the tile kernel takes; no residual
+    (8192, (5120,), True, False, True),              # no gain
+    (4096, (2048, 33, 96, 4000), False, False, False),
+]
+
+
+@pytest.mark.parametrize("K,Ns,res,gain,write_h", CASES)
+def test_fused_matches_two_calls(pkg, dev, K, Ns, res, gain, write_h):
+    print(f"rms-fused K={K} Ns={Ns} res={res} gain={gain} H={write_h}", flush=True)
+    g = torch.Generator().manual_seed(K + len(Ns))
+    X = (torch.randn(K, generator=g) * 3.0).to(dev)
+    R = (torch.randn(K, generator=g) * 0.5).to(dev) if res else None
+    gamma = (torch.rand(K, generator=g) + 0.5).to(dev) if gain else None
+    Ws = [pkg.synthetic_weights(K, N, seed=700 + i, device=dev) for i, N in enumerate(Ns)]
+    eps = 1e-6
+    H_ref = torch.empty(K, device=dev) if write_h else None
+    ws = pkg.rms_norm_q8_1(X, K, 1, residual=R, out_h=H_ref, gamma=gamma, eps=eps)
+    ref = pkg.mul_mat_q8_1_group(Ws, ws, K, list(Ns), 1)
+    H = torch.full((K,), float("nan"), device=dev) if write_h else None
+    for rep in range(2):  # twice: no state carried between calls
+        outs = pkg.rms_norm_mul_mat_group(Ws, X, K, list(Ns), residual=R, out_h=H, gamma=gamma, eps=eps)
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, ref)):
+            assert np.array_equal(bits(a), bits(b).ravel()), (rep, i)
+        if write_h:
+            assert np.array_equal(bits(H), bits(H_ref)), rep
+
+
+def test_fused_rejects(pkg, dev):
+    L = pkg.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    K, N = 5120, 64
+    W = pkg.synthetic_weights(K, N, seed=1, device=dev)
+    X = torch.randn(2 * K, device=dev)
+    Y = torch.empty(N, device=dev)
+    P1 = ctypes.c_void_p * 1
+    wp, yp, nn = P1(W.data_ptr()), P1(Y.data_ptr()), (ctypes.c_int64 * 1)(N)
+    inv, nsup = pkg.ERROR_INVALID_VALUE, pkg.ERROR_NOT_SUPPORTED
+    f = L.iq4xs_rms_norm_mul_mat_group
+    assert f(0, wp, yp, nn, X.data_ptr(), None, None, None, 1e-6, K, s) == inv
+    assert f(5, wp, yp, nn, X.data_ptr(), None, None, None, 1e-6, K, s) == inv
+    assert f(1, wp, yp, nn, None, None, None, None, 1e-6, K, s) == inv
+    assert f(1, wp, yp, nn, X.data_ptr(), None, None, None, -1.0, K, s) == inv
+    assert f(1, wp, yp, nn, X.data_ptr(), None, None, None, 1e-6, K + 32, s) == inv
+    # in place (H = X) and overlapping outputs are refused: workgroup 0 writes H while others read X
+    assert f(1, wp, yp, nn, X.data_ptr(), None, X.data_ptr(), None, 1e-6, K, s) == inv
+    assert f(1, wp, yp, nn, X.data_ptr(), None, X.data_ptr() + 4 * K - 16, None, 1e-6, K, s) == inv
+    yx = P1(X.data_ptr() + 4 * 16)
+    assert f(1, wp, yx, nn, X.data_ptr(), None, None, None, 1e-6, K, s) == inv
+    assert f(1, wp, yp, nn, X.data_ptr() + 4, None, None, None, 1e-6, K, s) == inv  # unaligned X
+    # shapes the fused prologue does not take
+    Ws = pkg.synthetic_weights(1024, N, seed=2, device=dev)
+    assert f(1, P1(Ws.data_ptr()), yp, nn, X.data_ptr(), None, None, None, 1e-6, 1024, s) == nsup
+    Xb = torch.randn(16640, device=dev)
+    Wb = pkg.synthetic_weights(16640, N, seed=3, device=dev)
+    assert f(1, P1(Wb.data_ptr()), yp, nn, Xb.data_ptr(), None, None, None, 1e-6, 16640, s) == nsup
+    torch.cuda.synchronize()
