@@ -178,9 +178,9 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
     token; bs=1 is M=1, prefill M=512):
         h += down_prev; A = Q8_1(rmsnorm(h) * g_attn)       iq4xs_rms_norm_q8_1
         q, k, v = W_q A, W_k A, W_v A                       iq4xs_mul_mat_q8_1
-        B = Q8_1(q)          (attention itself is outside this path: its
-                              output has q's shape and takes its place)
-        o = W_o B
+        o = W_o Q8_1(q)      iq4xs_mul_mat (attention itself is outside
+                              this path: its output has q's shape and takes
+                              its place)
         h += o; A = Q8_1(rmsnorm(h) * g_ffn)
         gate, up = W_gate A, W_up A
         C = Q8_1(silu(gate) * up)                           iq4xs_swiglu_q8_1
@@ -250,9 +250,10 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
                     else:
                         for i in range(3):
                             mm(Wl[i], wsA, *SHAPES[i])
-                L.check("iq4xs_quantize_q8_1", bufs["q_proj"].data_ptr(), Q_DIM, M, pkg.LAYOUT_MK, wsB.data_ptr(),
-                        wsB.numel(), s)
-                mm(Wl[3], wsB, *SHAPES[3])
+                # o from fp32 q (the stand-in for attention's output): iq4xs_mul_mat quantises it, in the
+                # GEMV's prologue at bs=1 (K = 8192), in its own launch for prefill
+                L.check("iq4xs_mul_mat", Wl[3].data_ptr(), bufs["q_proj"].data_ptr(), bufs["o_proj"].data_ptr(),
+                        Q_DIM, SHAPES[3][2], M, pkg.LAYOUT_MK, wsB.data_ptr(), wsB.numel(), s)
                 if fused:  # h_alt + o -> h, norm, gate/up: one launch
                     rms_group(l, 1, h_alt, bufs["o_proj"], h)
                 else:
