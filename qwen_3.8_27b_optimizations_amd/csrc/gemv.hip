@@ -17,7 +17,9 @@
 //       few whole rows; waves interleave the tile's steps, so the grid sweeps
 //       the matrix in address order; a ring of D register buffers keeps D-1
 //       steps in flight during compute; super-block partials meet in LDS and
-//       rows are summed in a fixed order.
+//       rows are summed in a fixed order.  Its prologue can also quantise
+//       fp32 activations (kFuse) or run the RMS-norm producer on one column
+//       (kRms, grouped launches) straight into its LDS operand.
 //   gemv_flat_kernel   (when the tile's LDS would not fit, e.g. 8 columns at
 //       K = 5120): each wave streams one contiguous range of steps and reduces
 //       a row whenever it ends (DPP), row pieces meet in LDS.
