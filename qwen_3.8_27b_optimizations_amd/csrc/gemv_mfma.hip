@@ -27,9 +27,12 @@
 // nibbles of qs bytes 8h .. 8h+7 of the sub-block (sub-block weights
 // 8h .. 8h+7 and 16+8h .. 16+8h+7), decoded in registers, and the A lanes the
 // activation codes of the same 16 weights.  The C element e of lane l is
-// token 8*(e>>2) + 4h + (e&3) of that row.  Token scales are staged in LDS
-// once ([sub-block][8]).  The GM_WAVES partial sums of every output are
-// added in LDS in wave order (deterministic).
+// token 8*(e>>2) + 4h + (e&3) of that row.  The token scales of a
+// super-block ride in the activation ring (one ds word per lane) and are
+// staged with its codes, so no workgroup-wide prologue or barrier precedes
+// the stream (staging every column scale up front measured 3-12 % slower).
+// The GM_WAVES partial sums of every output are added in LDS in wave order
+// (deterministic).
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 
@@ -39,7 +42,9 @@ constexpr int GM_LDS_MAX = 160 * 1024;
 
 constexpr int GM_AROW = 272;  // LDS row of one token's 256 codes, padded (bank spread)
 constexpr int GM_WROW = 144;  // LDS row of one weight row's 128 qs bytes, padded
-constexpr int GM_WAVE_LDS = 32 * GM_WROW + 8 * GM_AROW;  // per-wave staging bytes
+// per-wave staging bytes: weight rows, token rows, then the super-block's
+// column scales [8 sub-blocks][8 tokens]
+constexpr int GM_WAVE_LDS = 32 * GM_WROW + 8 * GM_AROW + 8 * 8 * 4;
 // Register ring of weight super-blocks per wave (one in flight while one is
 // computed); the activations, read by every workgroup and so L2-resident,
 // have a ring of their own, also one super-block ahead.  Depths 3 and 4
@@ -52,6 +57,7 @@ struct GmW {      // weights of one super-block (from HBM: the deep ring)
 };
 struct GmA {      // activations of one super-block (L2-resident: one ahead)
     v4i a[2];    // 32 of the super-block's activation codes: token lane/8, bytes 32*(lane%8) ..
+    uint32_t ds; // Q8_1 ds word of token lane/8, sub-block lane%8
 };
 
 template <int GM_WAVES, bool kDebug>
@@ -64,8 +70,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     constexpr int G = 1;  // M <= 8: tokens 4h + e of element e < 4
     extern __shared__ __attribute__((aligned(16))) float gm_lds[];
     const int bpr = K / QK_K, nb = K / QK8_1;
-    float* sdx = gm_lds;                        // [nb][8G] column scales, 0 past M
-    float* red = gm_lds + (size_t)nb * 8 * G;   // [GM_WAVES][4G][64] partial sums
+    float* red = gm_lds;                        // [GM_WAVES][4G][64] partial sums
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, col = lane & 31;
     uint8_t* swave = reinterpret_cast<uint8_t*>(red + GM_WAVES * 4 * G * 64) + (tid >> 6) * GM_WAVE_LDS;
     uint8_t* sw = swave;                                          // [32][144] qs of the 32 rows
@@ -88,11 +93,10 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     const uint32_t off_a = (uint32_t)min(lane >> 3, M - 1) * (uint32_t)K + 32 * (lane & 7);
     int8_t* awrite = sact + (lane >> 3) * GM_AROW + 32 * (lane & 7);
     const int8_t* aread = sact + min(col, M - 1) * GM_AROW + 8 * h;
-
-    for (int i = tid; i < nb * 8 * G; i += 64 * GM_WAVES) {
-        const int s = i / (8 * G), t = i - s * 8 * G;
-        sdx[i] = t < M ? half_bits_to_float(ads[(size_t)t * nb + s] & 0xFFFFu) : 0.0f;
-    }
+    // the current super-block's column scales, [sub-block][token] (0 past M),
+    // and this lane's ds word in every super-block: token lane/8, sub-block lane%8
+    float* sdx = reinterpret_cast<float*>(sact + 8 * GM_AROW);
+    const uint32_t off_d = (uint32_t)min(lane >> 3, M - 1) * (uint32_t)nb + (lane & 7);
 
     const int my_n = wave < bpr ? (bpr - wave + GM_WAVES - 1) / GM_WAVES : 0;
     auto load_w = [&](GmW& p, int kb) {
@@ -105,6 +109,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
         const int8_t* ak = aqs + (size_t)kb * QK_K;               // uniform
         p.a[0] = *reinterpret_cast<const v4i*>(ak + off_a);
         p.a[1] = *reinterpret_cast<const v4i*>(ak + off_a + 16);
+        p.ds = ads[(size_t)kb * 8 + off_d];
     };
 
     float acc[4 * G];
@@ -116,6 +121,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
         // previous super-block's reads were issued before these writes)
         *reinterpret_cast<v4i*>(awrite) = pa.a[0];
         *reinterpret_cast<v4i*>(awrite + 16) = pa.a[1];
+        sdx[(lane & 7) * 8 + (lane >> 3)] = (lane >> 3) < M ? half_bits_to_float(pa.ds & 0xFFFFu) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(wwrite + 8 * i * GM_WROW) = p.q[i];
         const float dw = half_bits_to_float(p.h.x & 0xFFFFu);
@@ -132,7 +138,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
             const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
             const int ls = subblock_ls(p.h.x, p.h.y, s) - 32;
             const float sa = dw * (float)ls;
-            const float* bxp = sdx + (kb * 8 + s) * 8 * G + 4 * h;
+            const float* bxp = sdx + s * 8 + 4 * h;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const v4f bx = *reinterpret_cast<const v4f*>(bxp + 8 * g);
@@ -161,7 +167,6 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
         for (int d = 0; d < GM_RING - 1; ++d) load_w(wb[d], wave + GM_WAVES * min(d, my_n - 1));
         load_a(ab[0], wave);
     }
-    __syncthreads();  // column scales staged
     for (int i0 = 0; i0 < my_n; i0 += UNR) {
 #pragma unroll
         for (int d = 0; d < UNR; ++d) {
@@ -190,11 +195,9 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
 template <int WAVES>
 static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
                             int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
-    const size_t lds = ((size_t)(K / QK8_1) * 8 + (size_t)WAVES * 4 * 64) * sizeof(float) +
-                       (size_t)WAVES * GM_WAVE_LDS;
+    const size_t lds = (size_t)WAVES * 4 * 64 * sizeof(float) + (size_t)WAVES * GM_WAVE_LDS;
     if (lds > GM_LDS_MAX) return hipErrorNotSupported;
     // the kernel's 32-bit load offsets span one 32-row block and 8 token rows
-    // (the LDS budget above already keeps K far below this)
     if ((int64_t)32 * (K / QK_K) * BLOCK_BYTES >= ((int64_t)1 << 31) || (int64_t)8 * K >= ((int64_t)1 << 31))
         return hipErrorNotSupported;
     if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit of a launch
