@@ -614,7 +614,17 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63, slot = lane >> 3, ib = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r0 = ((int)blockIdx.x - tile0) * rows_per_wg;
+    // Single-matrix launches take their tiles in XCD-contiguous ranges:
+    // workgroups are dispatched to the 8 XCDs round-robin (b -> XCD b % 8),
+    // and XCD x gets tiles [x*q + min(x, r), ...) of the G = 8q + r (a
+    // bijection).  Measured on the bs=1 decode set: -1.8 % per launch; grouped
+    // launches measured 2 % slower with it and keep the dispatch order.
+    int bid = (int)blockIdx.x;
+    if (!kGroup) {
+        const int G = (int)gridDim.x, q = G >> 3, r = G & 7, x = bid & 7;
+        bid = x * q + min(x, r) + (bid >> 3);
+    }
+    const int r0 = (bid - tile0) * rows_per_wg;
     const int nrows = min(rows_per_wg, N - r0);
     const int n_sb = nrows * bpr;
     const int n_steps = (n_sb + 7) >> 3;
