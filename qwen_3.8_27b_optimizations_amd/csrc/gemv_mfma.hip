@@ -15,7 +15,8 @@
 // with M: decoding the codes into the B operand, then per useful output a
 // convert, a scale product and a fused add.
 //
-// Mapping.  A workgroup of GM_WAVES (8 or 16) waves owns 32 weight rows; its waves take
+// Mapping.  A workgroup of GM_WAVES (8 or 16) waves owns up to 32 weight rows
+// (one MFMA block; rows past its own are masked); its waves take
 // the super-blocks kb = wave, wave + GM_WAVES, ... (at any moment they stream
 // GM_WAVES consecutive super-blocks of the same rows), each wave keeping one
 // super-block of loads in flight while it computes the previous one.  Its
@@ -65,7 +66,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
                                                                   const int8_t* __restrict__ aqs,
                                                                   const uint32_t* __restrict__ ads,
                                                                   float* __restrict__ Y, int K, int N, int M,
-                                                                  int64_t ldy_m, int64_t ldy_n,
+                                                                  int rows, int64_t ldy_m, int64_t ldy_n,
                                                                   int32_t* __restrict__ dbg) {
     constexpr int G = 1;  // M <= 8: tokens 4h + e of element e < 4
     extern __shared__ __attribute__((aligned(16))) float gm_lds[];
@@ -76,17 +77,19 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     uint8_t* sw = swave;                                          // [32][144] qs of the 32 rows
     int8_t* sact = reinterpret_cast<int8_t*>(swave + 32 * GM_WROW);  // [8][272] activations
     const int wave = tid >> 6;
-    const int r0 = blockIdx.x * 32;
+    const int r0 = blockIdx.x * rows;
+    const int nrow = min(rows, N - r0);  // this workgroup's rows (1..32; MFMA rows past them are masked)
     // Global loads are 32-bit lane offsets from workgroup-uniform bases (a
     // 32-row block spans 32 * K/256 * 136 bytes), which keeps the load ring
-    // in VGPRs.  Rows past N are clamped: computed, never stored.
+    // in VGPRs.  MFMA rows past nrow are clamped to its last row (a repeat
+    // of bytes already loaded, so no extra HBM traffic): computed, never stored.
     const uint32_t row_bytes = (uint32_t)bpr * BLOCK_BYTES;
     const uint8_t* wbase = W + (size_t)r0 * row_bytes;
-    const uint32_t off_h = (uint32_t)min(col, N - 1 - r0) * row_bytes;   // this lane's row (header)
+    const uint32_t off_h = (uint32_t)min(col, nrow - 1) * row_bytes;     // this lane's row (header)
     uint32_t off_q[4];                                                    // rows lane/8 + 8i, qs chunk lane%8
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        off_q[i] = (uint32_t)min((lane >> 3) + 8 * i, N - 1 - r0) * row_bytes + 8 + 16 * (lane & 7);
+        off_q[i] = (uint32_t)min((lane >> 3) + 8 * i, nrow - 1) * row_bytes + 8 + 16 * (lane & 7);
     uint8_t* wwrite = sw + (lane >> 3) * GM_WROW + 16 * (lane & 7);
     const uint8_t* wread = sw + col * GM_WROW + 8 * h;
     // this lane's share of a super-block's activations, and its MFMA A row in LDS
@@ -148,7 +151,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
                     acc[e] = __builtin_fmaf((float)c[e], sa * bx[j], acc[e]);
                     if (kDebug) {
                         const int t = 8 * g + 4 * h + j;
-                        if (t < M && r0 + col < N) dbg[((size_t)t * N + r0 + col) * nb + kb * 8 + s] = c[e] * ls;
+                        if (t < M && col < nrow) dbg[((size_t)t * N + r0 + col) * nb + kb * 8 + s] = c[e] * ls;
                     }
                 }
             }
@@ -180,7 +183,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
 #pragma unroll
     for (int e = 0; e < 4 * G; ++e) red[(wave * 4 * G + e) * 64 + lane] = acc[e];
     __syncthreads();
-    if (wave == 0 && r0 + col < N) {
+    if (wave == 0 && col < nrow) {
 #pragma unroll
         for (int e = 0; e < 4 * G; ++e) {
             float v = red[e * 64 + lane];
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
 
 template <int WAVES>
 static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
-                            int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+                            int64_t M, int rows, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     const size_t lds = (size_t)WAVES * 4 * 64 * sizeof(float) + (size_t)WAVES * GM_WAVE_LDS;
     if (lds > GM_LDS_MAX) return hipErrorNotSupported;
     // the kernel's 32-bit load offsets span one 32-row block and 8 token rows
@@ -208,13 +211,14 @@ static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t*
                                     hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS_MAX);
         if (e != hipSuccess) return e;
     }
-    const dim3 grid((unsigned)((N + 31) / 32)), block(64 * WAVES);
+    if (rows < 1 || rows > 32) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((N + rows - 1) / rows)), block(64 * WAVES);
     if (dbg)
         hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, true>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N,
-                           (int)M, ldy_m, ldy_n, dbg);
+                           (int)M, rows, ldy_m, ldy_n, dbg);
     else
         hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, false>), grid, block, lds, stream, W, aqs, ads, Y, (int)K,
-                           (int)N, (int)M, ldy_m, ldy_n, dbg);
+                           (int)N, (int)M, rows, ldy_m, ldy_n, dbg);
     return hipGetLastError();
 }
 
@@ -234,12 +238,24 @@ hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t*
                             int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     clear_launch_error();
     if (M < 1 || M > 8 || K % QK_K || K >= (1 << 24) || N >= (1 << 30)) return hipErrorNotSupported;
-    // Parallelism comes from splitting K over the waves of a 32-row block:
-    // with fewer blocks than two per CU, 16 waves each (measured: q, o and
+    // Parallelism comes from splitting K over the waves of a row block: with
+    // fewer 32-row blocks than two per CU, 16 waves each (measured: q, o and
     // down 5-15 % faster), otherwise 8 (gate/up: 16 would leave fewer
-    // workgroups resident per CU).
-    if ((N + 31) / 32 < 2 * gm_cu_count()) return launch_gm<16>(W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
-    return launch_gm<8>(W, aqs, ads, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
+    // workgroups resident per CU).  A row's arithmetic depends only on that
+    // wave count.  With 16 waves the rows per workgroup (at most 32, the
+    // MFMA's) are chosen so that every CU gets the same number of workgroups:
+    // N = 5120 takes 20 rows on 256 CUs instead of 160 blocks of 32 that
+    // leave 96 CUs idle (bs = 8: down 21.3 -> 18.4-19.5 us, o unchanged).
+    // Each workgroup decodes all 32 MFMA rows whatever it keeps, so the
+    // 8-wave shapes stay at 32 rows (gate with 17-row workgroups, 4 per CU
+    // instead of 2.125: 18.9 -> 21.5 us).
+    const int64_t cus = gm_cu_count();
+    if ((N + 31) / 32 < 2 * cus) {
+        const int64_t k = (N + 32 * cus - 1) / (32 * cus);
+        const int rows = (int)((N + cus * k - 1) / (cus * k));
+        return launch_gm<16>(W, aqs, ads, Y, K, N, M, rows, ldy_m, ldy_n, dbg, stream);
+    }
+    return launch_gm<8>(W, aqs, ads, Y, K, N, M, 32, ldy_m, ldy_n, dbg, stream);
 }
 
 }  // namespace iq4xs
