@@ -609,7 +609,7 @@ def main() -> int:
                    "step_spread": step_stats},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_tile_kernel<1,2,false,false,false> (bs=1, prequantised Q8_1)",
+                     "kernel": "iq4xs::gemv_tile_kernel<1, 2, false, false, false, 0> (bs=1, prequantised Q8_1)",
                      "avg_launch_us": round(avg_launch_us, 3), "launches_timed": n_launch * args.roofline_reps,
                      "launch_spread": launch_stats},
         "grouped_gemv": grouped,
