@@ -497,6 +497,32 @@ hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads,
     const int64_t gx = (N + (big ? G2_BN : GEMM_BN) - 1) / (big ? G2_BN : GEMM_BN);
     if (gx > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     grp.tile_end[0] = (int)gx;
+    if (big && dbg == nullptr) {
+        // Big tiles whose last round on the CUs would hold only a few (at most
+        // a quarter): the rows of that round go to the 64x64 kernel in a
+        // second launch, whose small tiles spread them over the chip.  Both
+        // kernels give bit-identical outputs.  M = 512 gate/up: 544 tiles =
+        // 2 full rounds + 32 on 256 CUs.
+        const int64_t gy = (M + G2_BM - 1) / G2_BM;
+        const int64_t cus = gemm_cu_count();
+        const int64_t full = gx * gy / cus, rem = gx * gy - full * cus;
+        if (full >= 1 && rem > 0 && 4 * rem <= cus && (full * cus) % gy == 0) {
+            const int64_t gx_big = full * cus / gy;  // whole N-tiles, every token tile
+            const int64_t n_big = gx_big * G2_BN;    // < N, since rem > 0
+            grp.N[0] = n_big;
+            grp.tile_end[0] = (int)gx_big;
+            const hipError_t e = launch_gemm_kernel<false, false>(true, grp, gx_big, aqs, ads, K, M, ldy_n, dbg, stream);
+            if (e != hipSuccess) return e;
+            GemmGroup rest{};
+            rest.W[0] = W + n_big * ((K / QK_K) * BLOCK_BYTES);
+            rest.Y[0] = Y + n_big * ldy_n;
+            rest.N[0] = N - n_big;
+            rest.ldy_m[0] = ldy_m;
+            const int64_t gx_rest = (N - n_big + GEMM_BN - 1) / GEMM_BN;
+            rest.tile_end[0] = (int)gx_rest;
+            return launch_gemm_kernel<false, false>(false, rest, gx_rest, aqs, ads, K, M, ldy_n, dbg, stream);
+        }
+    }
     return dbg ? launch_gemm_kernel<true, false>(big, grp, gx, aqs, ads, K, M, ldy_n, dbg, stream)
                : launch_gemm_kernel<false, false>(big, grp, gx, aqs, ads, K, M, ldy_n, dbg, stream);
 }

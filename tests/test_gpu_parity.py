@@ -269,7 +269,11 @@ GEMM_CASES = [(256, 64, 64), (256, 1, 1), (512, 100, 20), (768, 130, 65), (1024,
               # grids of >= 144 tiles of 128x128 take the double-buffered 128x128 kernel
               # (its debug instantiation included): one super-block per row; then an odd
               # super-block count with ragged rows and tokens
-              (256, 128 * 148, 64), (768, 128 * 145 + 33, 33)]
+              (256, 128 * 148, 64), (768, 128 * 145 + 33, 33),
+              # more than one round of 128x128 tiles on 256 CUs with a short last round: its rows
+              # go to the 64x64 kernel in a second launch (the debug export keeps one launch, so
+              # the equality with it below pins the split bit for bit)
+              (256, 128 * 276 + 5, 100), (256, 128 * 68 + 7, 512)]
 
 
 @pytest.mark.parametrize("K,N,M", GEMM_CASES)
