@@ -222,10 +222,13 @@ int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64
 
 /* Several weight matrices (1 <= count <= 4, each N[i] x K) against the same
  * quantised activations in ws: Y[i] = W[i] * dequant(ws), Y[i] laid out as
- * `layout` selects.  One launch covers every matrix: for M <= 8 the GEMV
- * (q/k/v, gate/up of a decode step), which pays the per-launch fixed cost
- * once; for M > 8 the GEMM, whose small matrices then fill the CUs that the
- * big ones' last round of tiles leaves idle.  Each output is bit-identical to
+ * `layout` selects.  For M <= 8 one launch of the streaming GEMV covers
+ * every matrix (q/k/v, gate/up of a decode step) and pays the per-launch
+ * fixed cost once; a matrix that takes the matrix-core GEMV (M >= 4 and
+ * N >= 2048) makes it one launch per matrix.  For M > 8 one GEMM launch, whose
+ * small matrices fill the CUs that the big ones' last round of tiles leaves
+ * idle (a short last round lying in the last matrix is a second launch of
+ * the small-tile kernel).  Each output is bit-identical to
  * iq4xs_mul_mat_q8_1 (path AUTO) on its own matrix.  W, Y, N are host arrays
  * of count entries.  No
  * counterpart in the reference, which runs every projection as its own

@@ -527,9 +527,10 @@ hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads,
                : launch_gemm_kernel<false, false>(big, grp, gx, aqs, ads, K, M, ldy_n, dbg, stream);
 }
 
-// One launch for `count` matrices sharing K and the activations: the tile
-// size is chosen for the summed rows, so the small matrices fill CUs that
-// the big ones' last round leaves idle.
+// One launch for `count` matrices sharing K and the activations (two when a
+// short last round is split off, below): the tile size is chosen for the
+// summed rows, so the small matrices fill CUs that the big ones' last round
+// leaves idle.
 hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N, const int8_t* aqs,
                              const uint32_t* ads, int64_t K, int64_t M, bool layout_mk, hipStream_t stream) {
     clear_launch_error();
@@ -549,6 +550,36 @@ hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y
         grp.N[i] = N[j];
         grp.ldy_m[i] = layout_mk ? N[j] : 1;
         grp.tile_end[i] = (int)tiles;
+    }
+    if (big) {
+        // As for single calls: a short last round of big tiles, when it lies
+        // in the last matrix, becomes a 64x64 launch over that matrix's
+        // trailing rows (M = 512 gate+up: 1088 tiles = 4 rounds + 64).
+        const int64_t gy = (M + G2_BM - 1) / G2_BM;
+        const int64_t cus = gemm_cu_count();
+        const int64_t full = tiles * gy / cus, rem = tiles * gy - full * cus;
+        const int last = count - 1;
+        const int64_t first_last = last > 0 ? grp.tile_end[last - 1] : 0;  // the last matrix's first N-tile
+        if (full >= 1 && rem > 0 && 4 * rem <= cus && (full * cus) % gy == 0 && full * cus / gy > first_last) {
+            const int64_t t_big = full * cus / gy;                 // N-tiles of the grouped launch
+            const int64_t n_keep = (t_big - first_last) * G2_BN;  // rows of the last matrix it keeps (< N)
+            for (int i = last; i < GEMV_GROUP_MAX; ++i) {
+                grp.N[i] = n_keep;
+                grp.tile_end[i] = (int)t_big;
+            }
+            const hipError_t e =
+                launch_gemm_kernel<false, true>(true, grp, t_big, aqs, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
+            if (e != hipSuccess) return e;
+            GemmGroup rest{};
+            rest.W[0] = W[last] + n_keep * ((K / QK_K) * BLOCK_BYTES);
+            rest.Y[0] = Y[last] + n_keep * (layout_mk ? 1 : M);
+            rest.N[0] = N[last] - n_keep;
+            rest.ldy_m[0] = layout_mk ? N[last] : 1;
+            const int64_t gx_rest = (N[last] - n_keep + GEMM_BN - 1) / GEMM_BN;
+            rest.tile_end[0] = (int)gx_rest;
+            return launch_gemm_kernel<false, false>(false, rest, gx_rest, aqs, ads, K, M, layout_mk ? 1 : M, nullptr,
+                                                    stream);
+        }
     }
     return launch_gemm_kernel<false, true>(big, grp, tiles, aqs, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
 }
