@@ -7,7 +7,7 @@
 //
 // Two kernels share this scheme (the launcher picks one per shape):
 // gemm_iq4xs_db_kernel (128x128 tile, 16 waves, double-buffered LDS) and
-// gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves, four per CU).
+// gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves, three per CU).
 //
 // Both are VALU-issue bound.  Every output needs its own scale per sub-block,
 // d_w[n] * d_x[m], so the epilogue costs VALU work per output and sub-block
@@ -435,20 +435,8 @@ static int gemm_kind() {
     return kind;
 }
 
-static int gemm_cu_count() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 // The 128x128 kernel runs one workgroup per CU and is faster per tile; the
-// 64x64 kernel (four per CU) wins when big tiles would leave many CUs idle:
+// 64x64 kernel (three per CU) wins when big tiles would leave many CUs idle:
 // fewer tiles than ~9/16 of the CUs (k/v-sized matrices).  Both give
 // bit-identical outputs, so this choice is a speed choice only (thresholds
 // from measurements on the 27B-class shapes at M = 512 / 2048).
@@ -457,7 +445,7 @@ static bool use_big_tiles(int64_t N, int64_t M, int64_t K) {
     if ((int64_t)G2_BN * (K / QK_K) * BLOCK_BYTES >= (1ll << 32) || (int64_t)G2_BM * K >= (1ll << 32)) return false;
     const int k = gemm_kind();
     if (k == 0 || k == 1) return k == 1;
-    const int64_t cus = gemm_cu_count();
+    const int64_t cus = device_cu_count();
     const int64_t tiles = ((N + G2_BN - 1) / G2_BN) * ((M + G2_BM - 1) / G2_BM);
     return tiles >= cus * 9 / 16;
 }
@@ -504,7 +492,7 @@ hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads,
         // kernels give bit-identical outputs.  M = 512 gate/up: 544 tiles =
         // 2 full rounds + 32 on 256 CUs.
         const int64_t gy = (M + G2_BM - 1) / G2_BM;
-        const int64_t cus = gemm_cu_count();
+        const int64_t cus = device_cu_count();
         const int64_t full = gx * gy / cus, rem = gx * gy - full * cus;
         if (full >= 1 && rem > 0 && 4 * rem <= cus && (full * cus) % gy == 0) {
             const int64_t gx_big = full * cus / gy;  // whole N-tiles, every token tile
@@ -556,7 +544,7 @@ hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y
         // in the last matrix, becomes a 64x64 launch over that matrix's
         // trailing rows (M = 512 gate+up: 1088 tiles = 4 rounds + 64).
         const int64_t gy = (M + G2_BM - 1) / G2_BM;
-        const int64_t cus = gemm_cu_count();
+        const int64_t cus = device_cu_count();
         const int64_t full = tiles * gy / cus, rem = tiles * gy - full * cus;
         const int last = count - 1;
         const int64_t first_last = last > 0 ? grp.tile_end[last - 1] : 0;  // the last matrix's first N-tile

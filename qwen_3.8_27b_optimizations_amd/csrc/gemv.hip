@@ -27,6 +27,7 @@
 //   gemv_global_kernel (activations too large for LDS): activations read
 //       through L1/L2.
 // Environment overrides for tuning (IQ4XS_GEMV_*) are read once per process.
+#include <atomic>
 #include <numeric>
 #include <stdlib.h>
 
@@ -785,16 +786,16 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
 constexpr int GEMV_WAVES_PER_WG = 8;
 constexpr size_t GEMV_LDS_BUDGET = 64 * 1024;
 
-static int device_cu_count() {
-    static int cached[64] = {0};
+int device_cu_count() {
+    static std::atomic<int> cached[64];  // static storage: starts at zero
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 
 template <int C, int IR>

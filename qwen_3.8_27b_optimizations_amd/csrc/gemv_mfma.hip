@@ -222,18 +222,6 @@ static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t*
     return hipGetLastError();
 }
 
-static int gm_cu_count() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K,
                             int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     clear_launch_error();
@@ -249,7 +237,7 @@ hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t*
     // Each workgroup decodes all 32 MFMA rows whatever it keeps, so the
     // 8-wave shapes stay at 32 rows (gate with 17-row workgroups, 4 per CU
     // instead of 2.125: 18.9 -> 21.5 us).
-    const int64_t cus = gm_cu_count();
+    const int64_t cus = device_cu_count();
     if ((N + 31) / 32 < 2 * cus) {
         const int64_t k = (N + 32 * cus - 1) / (32 * cus);
         const int rows = (int)((N + cus * k - 1) / (cus * k));

@@ -11,6 +11,11 @@ namespace iq4xs {
 // its own launches' status with hipGetLastError.
 inline void clear_launch_error() { (void)hipGetLastError(); }
 
+// Compute units of the current device, queried once per device (256 when the
+// query fails); launchers size their grids with it.  Safe to call from any
+// host thread.
+int device_cu_count();
+
 // Activation / output layouts.
 constexpr int LAYOUT_KM = 0;  // X[k*M+m], Y[n*M+m]   (standalone API)
 constexpr int LAYOUT_MK = 1;  // X[m*K+k], Y[m*N+n]   (ggml src1 / dst)
