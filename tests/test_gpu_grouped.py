@@ -33,6 +33,9 @@ GROUP_CASES = [  # K, Ns, M, layout
     (5120, (8192, 1024, 1024), 512, LAYOUT_MK),   # q alone takes 128x128 tiles, the group 64x64 ones
     (5120, (17408, 17408), 512, LAYOUT_KM),       # gate/up: 64x64 alone, 128x128 as a group
     (8192, (130, 4000, 64), 200, LAYOUT_MK),      # ragged tiles in every matrix
+    # 271 big tiles on 256 CUs: the short last round lies in the second matrix, whose
+    # trailing 1797 rows go to a small-tile launch (token-major outputs, ragged rows)
+    (256, (128 * 200, 128 * 70 + 5), 100, LAYOUT_KM),
 ]
 
 
