@@ -293,6 +293,35 @@ def test_gemm_sums_and_outputs(pkg, orc, dev, K, N, M):
     assert torch.equal(Ykm.T, Y2)
 
 
+# fp16 super-block scales at the edges of the format: zero, the smallest subnormal, the
+# smallest normal, one, the largest finite, and negatives of some (bit patterns)
+EXTREME_D = np.array([0x0000, 0x0001, 0x0400, 0x3C00, 0x7BFF, 0x8400, 0x8001, 0xFBFF], np.uint16)
+
+
+# N, M: bs=1 tile GEMV, matrix-core GEMV (M = 4, 8), 64x64 GEMM, 128x128 GEMM (146 tiles)
+@pytest.mark.parametrize("N,M", [(2051, 1), (2051, 4), (2051, 8), (2051, 100), (128 * 145 + 3, 64)])
+def test_extreme_weight_scales(pkg, orc, dev, N, M):
+    """Each kernel family on weights whose fp16 d spans zero, subnormals and the largest
+    finite values: the sub-block sums stay bit-exact and the outputs match the reference
+    semantics."""
+    K = 2048
+    W = orc.gen_weights(K, N, seed=77)
+    blocks = W.reshape(-1, 136)
+    d = np.resize(EXTREME_D, blocks.shape[0])
+    blocks[:, 0] = (d & 0xFF).astype(np.uint8)
+    blocks[:, 1] = (d >> 8).astype(np.uint8)
+    X = orc.gen_activations(K * M, seed=78, outliers=True).reshape(M, K)
+    AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
+    Wd = D(W, dev)
+    ws = pkg.quantize_q8_1(D(X, dev), K, M, LAYOUT_MK)
+    S, Y = pkg.subblock_sums(Wd, ws, K, N, M, pkg.PATH_GEMV if M <= 8 else pkg.PATH_GEMM)
+    Y2 = pkg.mul_mat_q8_1(Wd, ws, K, N, M, LAYOUT_MK)  # path AUTO: the same kernel
+    torch.cuda.synchronize()
+    assert np.array_equal(S.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, M))
+    assert torch.equal(Y, Y2)
+    assert bool(torch.isfinite(Y).all())
+    check_outputs(orc, W, AQ, Y.cpu().numpy(), K, N, M, f"extreme d, M={M}")
+
 def test_gemv_and_gemm_paths_agree(pkg, orc, dev):
     K, N, M = 2048, 256, 8
     W = D(orc.gen_weights(K, N, seed=5), dev)
