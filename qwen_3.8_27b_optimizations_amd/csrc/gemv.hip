@@ -187,16 +187,20 @@ __device__ inline void stage_activations(const int8_t* __restrict__ aqs, const u
 // issued before the weight prefetch and the quantisation + LDS writes after
 // it (vmcnt retires in order: x loaded after the weights would wait for
 // them).  Loads are unconditional (index clamped): loads inside divergent
-// branches make the compiler's wait counts conservative.  Needs K/4 <= 4 *
-// threads.
+// branches make the compiler's wait counts conservative, so every round is
+// issued: two rounds cover K <= 8 * threads (8192 for the 16-wave tile, the
+// fused bound), and fewer idle rounds keep the prologue short: four rounds,
+// two or more of them repeats at K <= 8192, measured 2 % slower on the bs=1
+// decode step.  Needs K/4 <= 2 * threads (longer rows take quantize_to_lds).
+constexpr int FUSED_ROUNDS = 2;
 struct FusedRegs {
-    float x[4][4];
+    float x[FUSED_ROUNDS][4];
 };
 
 __device__ inline void fused_load(FusedRegs& r, const float* __restrict__ X, int64_t sk, int tasks, int tid,
                                   int nthreads) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < FUSED_ROUNDS; ++u) {
         const int t = min(tid + u * nthreads, tasks - 1);  // clamped: the load is unconditional
         const float* p = X + (int64_t)((t >> 3) * QK8_1 + q8_lane_elem(t & 7)) * sk;
         r.x[u][0] = p[0];
@@ -208,7 +212,7 @@ __device__ inline void fused_load(FusedRegs& r, const float* __restrict__ X, int
 
 __device__ inline void fused_store(const FusedRegs& r, int8_t* sq, float* sdx, int tasks, int tid, int nthreads) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < FUSED_ROUNDS; ++u) {
         const int t = tid + u * nthreads;
         if (t < tasks) {
             const int ib = t >> 3, j = q8_lane_elem(t & 7);
@@ -652,7 +656,7 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     // staged after the prefetch, below).
     const int nthreads = blockDim.x;
     const int tasks = K / 4;
-    const bool split = kFuse && C == 1 && tasks <= 4 * nthreads;
+    const bool split = kFuse && C == 1 && tasks <= FUSED_ROUNDS * nthreads;
     FusedRegs fx;
     if (split) fused_load(fx, X, sk, tasks, tid, nthreads);
     RmsBatch rb;  // the RMS prologue's pass-1 loads (one batch: K <= RMS_ONE_BATCH_K), also ahead of the prefetch
