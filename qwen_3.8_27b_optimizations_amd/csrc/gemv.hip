@@ -1060,7 +1060,7 @@ static void launch_rms_tile(dim3 grid, dim3 block, size_t lds, hipStream_t strea
 // workgroup runs the producer's passes on the whole row (h staged in LDS, the
 // Q8_1 codes straight into the GEMV's operand), workgroup 0 writes H.  The
 // codes, and so every output, are those of iq4xs_rms_norm_q8_1 followed by the
-// grouped GEMV.  hipErrorNotSupported past one pass-1 batch (K > 16384), below
+// grouped GEMV.  hipErrorNotSupported past one pass-1 batch (K > 8192), below
 // the tile kernel's K >= 2048, or when the LDS does not fit.
 hipError_t launch_gemv_rms_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
                                  const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,

@@ -17,7 +17,7 @@ namespace iq4xs {
 
 constexpr int RMS_THREADS = 1024;
 constexpr int RMS_WAVES = RMS_THREADS / 64;
-constexpr int RMS_BATCH = 4;
+constexpr int RMS_BATCH = 2;  // two rounds reach K = 8192 (rms at decode shapes); four measured 8 % slower
 // one pass-1 batch of a thread covers K up to this
 constexpr int64_t RMS_ONE_BATCH_K = 4 * (int64_t)RMS_THREADS * RMS_BATCH;
 
