@@ -145,8 +145,10 @@ int dequant_iq4xs_gpu(const void* src, float* dst, int64_t n_blocks, int warp_si
 /* ============================ ggml mul_mat boundary ============================ */
 
 /* Replaces custom_gemv_iq4xs_can_handle, patch:274-277.  True for
- * type == GGML_TYPE_IQ4_XS, 1 <= M <= 8, K > 0, K % 256 == 0, N > 0 (the
- * reference's K/N whitelist is dropped). */
+ * type == GGML_TYPE_IQ4_XS, M == 1 (custom_gemv_iq4xs_dispatch computes one
+ * column), K > 0, K % 256 == 0, N > 0 (the reference's K/N whitelist is
+ * dropped).  Batches of 2..8 columns are served by custom_gemm_iq4xs_dispatch,
+ * which routes them to the small-batch GEMV. */
 bool custom_gemv_iq4xs_can_handle(int64_t K, int64_t N, int64_t M, int type);
 
 /* Replaces custom_gemv_iq4xs_dispatch, patch:278-280 (called from the mmvq.cu

@@ -26,24 +26,36 @@ bool valid_mat(const void* W, const void* X, const void* Y, int64_t K, int64_t N
     return W && X && Y && valid_k(K) && N > 0 && M > 0 && K < MAX_DIM && N < MAX_DIM && M < MAX_DIM;
 }
 
-// The stream-ordered pool of each device keeps freed blocks instead of
-// returning them to the driver, so per-call scratch is a pool hit.
-std::once_flag g_pool_once[64];
+// Per-call Q8_1 scratch of the reference-named entry points comes from a
+// stream-ordered pool that this library creates for each device and owns.
+// The pool keeps freed blocks instead of returning them to the driver, so a
+// repeated call is a pool hit.  The device's default pool, which the rest of
+// the process (a host application, PyTorch) may use, is left untouched.
+constexpr int MAX_DEVICES = 64;
+std::once_flag g_pool_once[MAX_DEVICES];
+hipMemPool_t g_pool[MAX_DEVICES];
+hipError_t g_pool_err[MAX_DEVICES];
 
 hipError_t pool_alloc(void** p, size_t bytes, hipStream_t stream) {
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return err;
-    if (dev >= 0 && dev < 64) {
-        std::call_once(g_pool_once[dev], [dev]() {
-            hipMemPool_t pool;
-            if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-                uint64_t keep = UINT64_MAX;
-                (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-            }
-        });
-    }
-    return hipMallocAsync(p, bytes, stream);
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::call_once(g_pool_once[dev], [dev]() {
+        hipMemPoolProps props{};
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipError_t e = hipMemPoolCreate(&g_pool[dev], &props);
+        if (e == hipSuccess) {
+            uint64_t keep = UINT64_MAX;
+            e = hipMemPoolSetAttribute(g_pool[dev], hipMemPoolAttrReleaseThreshold, &keep);
+        }
+        g_pool_err[dev] = e;
+    });
+    if (g_pool_err[dev] != hipSuccess) return g_pool_err[dev];
+    return hipMallocFromPoolAsync(p, bytes, g_pool[dev], stream);
 }
 
 struct Planar {
@@ -221,9 +233,12 @@ int dequant_iq4xs_gpu(const void* src, float* dst, int64_t n_blocks, int warp_si
     return launch_dequant(static_cast<const uint8_t*>(src), dst, n_blocks, as_stream(stream));
 }
 
+// The dispatch below computes one column (it has no M argument), so the gate
+// accepts exactly M == 1, as the reference's does (patch:274-277); small
+// batches reach the GEMV through custom_gemm_iq4xs_dispatch and the explicit
+// API.
 bool custom_gemv_iq4xs_can_handle(int64_t K, int64_t N, int64_t M, int type) {
-    return type == IQ4XS_GGML_TYPE_IQ4_XS && M >= 1 && M <= GEMV_MAX_COLS && valid_k(K) && K < MAX_DIM && N > 0 &&
-           N < MAX_DIM;
+    return type == IQ4XS_GGML_TYPE_IQ4_XS && M == 1 && valid_k(K) && K < MAX_DIM && N > 0 && N < MAX_DIM;
 }
 
 int custom_gemv_iq4xs_dispatch(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream) {

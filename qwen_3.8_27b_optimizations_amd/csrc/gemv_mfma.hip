@@ -237,8 +237,15 @@ hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t*
     // Each workgroup decodes all 32 MFMA rows whatever it keeps, so the
     // 8-wave shapes stay at 32 rows (gate with 17-row workgroups, 4 per CU
     // instead of 2.125: 18.9 -> 21.5 us).
+    //
+    // The wave count fixes each row's fp32 summation order, so it is chosen
+    // from the shape alone, against MI355X's 256 CUs: a device or partition
+    // with another CU count gives the same bits.  The rows per workgroup only
+    // balance the grid (a row's arithmetic does not depend on them) and use
+    // the device's own CU count.
+    constexpr int64_t kWaveChoiceCus = 256;
     const int64_t cus = device_cu_count();
-    if ((N + 31) / 32 < 2 * cus) {
+    if ((N + 31) / 32 < 2 * kWaveChoiceCus) {
         const int64_t k = (N + 32 * cus - 1) / (32 * cus);
         const int rows = (int)((N + cus * k - 1) / (cus * k));
         return launch_gm<16>(W, aqs, ads, Y, K, N, M, rows, ldy_m, ldy_n, dbg, stream);

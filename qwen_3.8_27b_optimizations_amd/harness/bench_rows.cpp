@@ -1,0 +1,297 @@
+// bench_rows.cpp -- the reference's kernel bench harness on this library: JSON
+// arrays of per-shape rows with the reference's keys, so its archive tooling
+// (benchmarks/tools/run_kernel_bench.py:56-99) ingests them as it did the
+// gfx1100 binaries' output.  Each row's columns time the entry points of the
+// same names as the reference bench, called through the reference's own C++
+// signatures (include/iq4xs_reference_api.hpp):
+//
+//   --op gemv       bench_gemv.cpp:63-78        "gemv_iq4xs": stock =
+//                   gemv_iq4xs_stock_gpu, gfx1100 = gemv_iq4xs_gfx1100_gpu
+//                   (the FP64 comparators, as there)
+//   --op gemv_dp4a  bench_gemv_dp4a.cpp:110-133 "gemv_iq4xs_dp4a_coop":
+//                   real_dp4a = gemv_iq4xs_stock_dp4a_gpu, coop_dp4a =
+//                   gemv_iq4xs_dp4a_gfx1100_gpu (both this library's GEMV,
+//                   Q8_1 quantisation included)
+//   --op gemm_wmma  bench_gemm_wmma.cpp:216-256 "gemm_iq4xs_wmma_stream":
+//                   stock = gemm_iq4xs_stock_dp4a_gpu, tiled =
+//                   gemm_iq4xs_stream_tiled_gpu, one row per reference
+//                   variant name with its entry point (all run this
+//                   library's Q8_1 MFMA GEMM)
+//
+// Timing is bench.h's (bench_stats.h): 50 warm-up + 200 timed launches per
+// run for the GEMVs, 2 + 5 for the GEMMs, `--runs` runs folded as the
+// reference folds them.  Weights stay in one buffer, as in the reference
+// benches, so the 256 MB Infinity Cache can serve the smaller matrices'
+// repeats; bench.py's rotated legs are the HBM-streaming figures.
+//
+// --schema prints one row per op with zero statistics and touches no GPU
+// (the CPU tests compare its keys with the reference's); --stats-selftest
+// prints bench_stats_from() on a fixed sample.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "bench_stats.h"
+#include "iq4xs_reference_api.hpp"
+
+namespace {
+
+// An ordered JSON object written as the reference's benches print rows.
+struct Row {
+    std::vector<std::pair<std::string, std::string>> kv;
+    Row& s(const char* k, const std::string& v) {
+        kv.emplace_back(k, "\"" + v + "\"");
+        return *this;
+    }
+    Row& i(const char* k, long long v) {
+        kv.emplace_back(k, std::to_string(v));
+        return *this;
+    }
+    Row& f(const char* k, double v, int prec) {
+        char buf[64];
+        snprintf(buf, sizeof buf, "%.*f", prec, v);
+        kv.emplace_back(k, buf);
+        return *this;
+    }
+};
+
+bool g_first = true;
+
+void emit(const Row& r) {
+    printf(g_first ? "[\n  {\n" : ",\n  {\n");
+    g_first = false;
+    for (size_t j = 0; j < r.kv.size(); ++j)
+        printf("    \"%s\": %s%s\n", r.kv[j].first.c_str(), r.kv[j].second.c_str(), j + 1 < r.kv.size() ? "," : "");
+    printf("  }");
+    fflush(stdout);
+}
+
+struct Shape {
+    const char* name;
+    int64_t K, N;
+};
+// the reference's canonical shapes (kernels/matmul_iq4xs/ref_cpu.h:15-24), then
+// the 27B-class decode projections this library is measured on
+const Shape kGemvShapes[] = {{"attn_q", 5120, 5120},   {"attn_k", 5120, 5120},   {"attn_v", 5120, 5120},
+                             {"attn_gate", 5120, 6144}, {"attn_out", 5120, 5120}, {"ffn_gate", 5120, 17408},
+                             {"ffn_up", 5120, 17408},  {"ffn_down", 17408, 5120}, {"q_proj", 5120, 8192},
+                             {"k_proj", 5120, 1024},   {"v_proj", 5120, 1024},   {"o_proj", 8192, 5120}};
+// bench_gemm_wmma.cpp:96-101 shapes and M tiers (the 8192 tier, skipped there for
+// VRAM, runs here)
+const Shape kGemmShapes[] = {{"attn_q", 5120, 5120}, {"ffn_gate", 5120, 17408}, {"ffn_down", 17408, 5120}};
+const int64_t kGemmMs[] = {128, 512, 1024, 8192};
+
+struct Variant {
+    const char *name, *tile, *P, *banking;
+    hipError_t (*fn)(const block_iq4_xs*, const float*, float*, int64_t, int64_t, int64_t, hipStream_t);
+};
+hipError_t lut_no_table(const block_iq4_xs* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
+                        hipStream_t s) {
+    return gemm_iq4xs_lut_gpu(W, nullptr, X, Y, K, N, M, s);
+}
+// the reference's variant names (bench_gemm_wmma.cpp:89-95) with the entry point
+// each binds; here every one runs the same GEMM (128x128 or 64x64 int8-MFMA tiles
+// chosen per shape, double-buffered LDS, padded / XOR-swizzled rows)
+const Variant kVariants[] = {
+    {"64x32_P2+33", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_stream_gpu},
+    {"64x32_P4_XOR", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_p4_xor_gpu},
+    {"64x64_P4_XOR", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_64x64_gpu},
+    {"128x32", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_stream_gpu},
+    {"LUT_mu4", "128x128|64x64", "P=2", "pad272|xor", lut_no_table},
+};
+
+Row gemv_row(const Shape& sh, size_t bytes, const BenchStats& st, const BenchStats& gx) {
+    const double speedup = gx.median_us > 0 ? st.median_us / gx.median_us : 0.0;
+    Row r;
+    r.s("op", "gemv_iq4xs").s("shape", sh.name).i("K", sh.K).i("N", sh.N).i("M", 1).i("bytes", (long long)bytes);
+    r.f("stock_median_us", st.median_us, 3).f("stock_p95_us", st.p95_us, 3).f("stock_gb_s", st.gb_s, 2);
+    r.f("gfx1100_median_us", gx.median_us, 3).f("gfx1100_p95_us", gx.p95_us, 3).f("gfx1100_gb_s", gx.gb_s, 2);
+    r.f("speedup", speedup, 3).s("winner", speedup > 1.0 ? "gfx1100" : "stock");
+    return r;
+}
+
+Row gemv_dp4a_row(const Shape& sh, size_t bytes, int runs, const BenchStats& st, const BenchStats& co) {
+    const double sm = co.median_us > 0 ? st.median_us / co.median_us : 0.0;
+    const double smean = co.mean_us > 0 ? st.mean_us / co.mean_us : 0.0;
+    const double s1 = (co.mean_us + co.stdev_us) > 0 ? (st.mean_us - st.stdev_us) / (co.mean_us + co.stdev_us) : 0.0;
+    Row r;
+    r.s("op", "gemv_iq4xs_dp4a_coop").s("shape", sh.name).i("K", sh.K).i("N", sh.N).i("M", 1);
+    r.i("bytes", (long long)bytes).i("runs", runs).s("variant", "tile-wave64");
+    r.f("real_dp4a_median_us", st.median_us, 3).f("real_dp4a_mean_us", st.mean_us, 3);
+    r.f("real_dp4a_stddev_us", st.stdev_us, 3).f("real_dp4a_p95_us", st.p95_us, 3).f("real_dp4a_gb_s", st.gb_s, 2);
+    r.f("coop_dp4a_median_us", co.median_us, 3).f("coop_dp4a_mean_us", co.mean_us, 3);
+    r.f("coop_dp4a_stddev_us", co.stdev_us, 3).f("coop_dp4a_p95_us", co.p95_us, 3).f("coop_dp4a_gb_s", co.gb_s, 2);
+    r.f("speedup", sm, 3).f("speedup_median", sm, 3).f("speedup_mean", smean, 3);
+    r.f("speedup_mean_minus_1sigma", s1, 3).s("winner", sm > 1.0 ? "coop_dp4a" : "real_dp4a_stock");
+    r.s("note", "MI355X gfx950 wave64 tile GEMV (v_dot4, DPP row sums, Q8_1 quantised in the prologue for K <= 8192); "
+                "both columns call this library's GEMV");
+    return r;
+}
+
+Row gemm_row(const Shape& sh, int64_t M, size_t bytes, double flops, int runs, const Variant& v,
+             const BenchStats& st, const BenchStats& ti, const BenchStats& wm) {
+    const double tf = [&](double us) { return us > 0 ? flops / (us * 1e-6) / 1e12 : 0.0; }(wm.median_us);
+    const double tf_st = st.median_us > 0 ? flops / (st.median_us * 1e-6) / 1e12 : 0.0;
+    const double tf_ti = ti.median_us > 0 ? flops / (ti.median_us * 1e-6) / 1e12 : 0.0;
+    const double sp = wm.median_us > 0 ? st.median_us / wm.median_us : 0.0;
+    const double sp_mean = wm.mean_us > 0 ? st.mean_us / wm.mean_us : 0.0;
+    const double sp_1s = (wm.mean_us + wm.stdev_us) > 0 ? (st.mean_us - st.stdev_us) / (wm.mean_us + wm.stdev_us) : 0.0;
+    Row r;
+    r.s("op", "gemm_iq4xs_wmma_stream").s("shape", sh.name).i("K", sh.K).i("N", sh.N).i("M", M);
+    r.i("bytes", (long long)bytes).f("flops", flops, 0).i("runs", runs);
+    r.s("variant", v.name).s("tile", v.tile).s("P", v.P).s("banking", v.banking);
+    r.f("stock_median_us", st.median_us, 3).f("stock_mean_us", st.mean_us, 3).f("stock_stddev_us", st.stdev_us, 3);
+    r.f("stock_p95_us", st.p95_us, 3).f("stock_tflops", tf_st, 3).f("stock_gb_s", st.gb_s, 2);
+    r.f("tiled_median_us", ti.median_us, 3).f("tiled_tflops", tf_ti, 3);
+    r.f("wmma_median_us", wm.median_us, 3).f("wmma_mean_us", wm.mean_us, 3).f("wmma_stddev_us", wm.stdev_us, 3);
+    r.f("wmma_p95_us", wm.p95_us, 3).f("wmma_stream_median_us", wm.median_us, 3);
+    r.f("wmma_stream_p95_us", wm.p95_us, 3).f("wmma_stream_tflops", tf, 3).f("wmma_stream_gb_s", wm.gb_s, 2);
+    r.f("speedup", sp, 3).f("speedup_median", sp, 3).f("speedup_vs_stock_dp4a", sp, 3);
+    r.f("speedup_mean", sp_mean, 3).f("speedup_mean_minus_1sigma", sp_1s, 3).f("TFLOPS_median", tf, 3);
+    r.f("GB/s", wm.gb_s, 2).s("winner", sp > 1.0 ? "wmma_stream" : "stock_dp4a");
+    r.s("note", "MI355X gfx950 int8-MFMA GEMM on Q8_1 activations (the reference's fp16 WMMA numerics are not "
+                "reproduced); every variant name binds this library's GEMM");
+    return r;
+}
+
+#define CHECK(call)                                                                               \
+    do {                                                                                          \
+        const hipError_t e_ = (call);                                                             \
+        if (e_ != hipSuccess) {                                                                   \
+            fprintf(stderr, "%s:%d %s -> %s\n", __FILE__, __LINE__, #call, hipGetErrorString(e_)); \
+            return 2;                                                                             \
+        }                                                                                         \
+    } while (0)
+
+int run_gemv(bool dp4a, int runs, hipStream_t s) {
+    for (const Shape& sh : kGemvShapes) {
+        const int64_t nblk = sh.N * (sh.K / 256);
+        const size_t bytes = (size_t)nblk * 136 + (size_t)sh.K * 4 + (size_t)sh.N * 4;
+        void* W = nullptr;
+        float *x = nullptr, *y = nullptr;
+        CHECK(hipMalloc(&W, (size_t)nblk * 136));
+        CHECK(hipMalloc((void**)&x, (size_t)sh.K * 4));
+        CHECK(hipMalloc((void**)&y, (size_t)sh.N * 4));
+        CHECK((hipError_t)iq4xs_fill_synthetic_weights(W, nblk, 12345, 0, s));
+        CHECK((hipError_t)iq4xs_fill_synthetic_activations(x, sh.K, 42, 0, s));
+        const block_iq4_xs* Wb = static_cast<const block_iq4_xs*>(W);
+        auto a = [&](hipStream_t st) {
+            return dp4a ? gemv_iq4xs_stock_dp4a_gpu(Wb, x, y, sh.K, sh.N, st) : gemv_iq4xs_stock_gpu(Wb, x, y, sh.K, sh.N, st);
+        };
+        auto b = [&](hipStream_t st) {
+            return dp4a ? gemv_iq4xs_dp4a_gfx1100_gpu(Wb, x, y, sh.K, sh.N, st)
+                        : gemv_iq4xs_gfx1100_gpu(Wb, x, y, sh.K, sh.N, st);
+        };
+        std::vector<BenchStats> ra, rb;
+        for (int r = 0; r < (dp4a ? runs : 1); ++r) {
+            BenchStats sa, sb;
+            if (!bench_event(a, s, 50, 200, bytes, sa) || !bench_event(b, s, 50, 200, bytes, sb)) {
+                fprintf(stderr, "launch failed at %s\n", sh.name);
+                return 2;
+            }
+            ra.push_back(sa);
+            rb.push_back(sb);
+        }
+        if (dp4a)
+            emit(gemv_dp4a_row(sh, bytes, runs, bench_aggregate(ra), bench_aggregate(rb)));
+        else
+            emit(gemv_row(sh, bytes, ra[0], rb[0]));
+        CHECK(hipFree(W));
+        CHECK(hipFree(x));
+        CHECK(hipFree(y));
+    }
+    return 0;
+}
+
+int run_gemm(int runs, hipStream_t s) {
+    for (const Shape& sh : kGemmShapes) {
+        const int64_t nblk = sh.N * (sh.K / 256);
+        void* W = nullptr;
+        CHECK(hipMalloc(&W, (size_t)nblk * 136));
+        CHECK((hipError_t)iq4xs_fill_synthetic_weights(W, nblk, 7777, 0, s));
+        const block_iq4_xs* Wb = static_cast<const block_iq4_xs*>(W);
+        for (int64_t M : kGemmMs) {
+            const size_t bytes = (size_t)nblk * 136 + (size_t)(sh.K * M) * 4 + (size_t)(sh.N * M) * 4;
+            const double flops = 2.0 * (double)sh.N * (double)M * (double)sh.K;
+            float *X = nullptr, *Y = nullptr;
+            CHECK(hipMalloc((void**)&X, (size_t)(sh.K * M) * 4));
+            CHECK(hipMalloc((void**)&Y, (size_t)(sh.N * M) * 4));
+            CHECK((hipError_t)iq4xs_fill_synthetic_activations(X, sh.K * M, 42 + M, 0, s));
+            auto stock = [&](hipStream_t st) { return gemm_iq4xs_stock_dp4a_gpu(Wb, X, Y, sh.K, sh.N, M, st); };
+            auto tiled = [&](hipStream_t st) { return gemm_iq4xs_stream_tiled_gpu(Wb, X, Y, sh.K, sh.N, M, st); };
+            std::vector<BenchStats> rs, rt;
+            for (int r = 0; r < runs; ++r) {
+                BenchStats a, b;
+                if (!bench_event(stock, s, 2, 5, bytes, a)) return 2;
+                if (r == 0 && !bench_event(tiled, s, 1, 1, bytes, b)) return 2;
+                rs.push_back(a);
+                rt.push_back(r == 0 ? b : rt[0]);
+            }
+            const BenchStats st = bench_aggregate(rs), ti = bench_aggregate(rt);
+            for (const Variant& v : kVariants) {
+                auto launch = [&](hipStream_t q) { return v.fn(Wb, X, Y, sh.K, sh.N, M, q); };
+                std::vector<BenchStats> rv;
+                for (int r = 0; r < runs; ++r) {
+                    BenchStats c;
+                    if (!bench_event(launch, s, 2, 5, bytes, c)) return 2;
+                    rv.push_back(c);
+                }
+                emit(gemm_row(sh, M, bytes, flops, runs, v, st, ti, bench_aggregate(rv)));
+            }
+            CHECK(hipFree(X));
+            CHECK(hipFree(Y));
+        }
+        CHECK(hipFree(W));
+    }
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    std::string op = "gemv_dp4a";
+    int runs = 10;
+    bool schema = false;
+    for (int i = 1; i < argc; ++i) {
+        if (!strcmp(argv[i], "--op") && i + 1 < argc) op = argv[++i];
+        else if (!strcmp(argv[i], "--runs") && i + 1 < argc) runs = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--schema")) schema = true;
+        else if (!strcmp(argv[i], "--stats-selftest")) {
+            const BenchStats st = bench_stats_from({5.0, 1.0, 4.0, 2.0, 3.0, 10.0, 7.0, 6.0, 9.0, 8.0, 11.0}, 3, 1000000);
+            printf("{\"median_us\": %.6f, \"p95_us\": %.6f, \"min_us\": %.6f, \"max_us\": %.6f, \"mean_us\": %.6f, "
+                   "\"stdev_us\": %.6f, \"count\": %d, \"gb_s\": %.6f}\n",
+                   st.median_us, st.p95_us, st.min_us, st.max_us, st.mean_us, st.stdev_us, st.count, st.gb_s);
+            return 0;
+        } else {
+            fprintf(stderr, "usage: %s [--op gemv|gemv_dp4a|gemm_wmma] [--runs N] [--schema] [--stats-selftest]\n",
+                    argv[0]);
+            return 2;
+        }
+    }
+    if (runs < 1) runs = 1;
+    if (schema) {  // one zero-statistics row per op: no GPU is touched
+        const BenchStats z;
+        emit(gemv_row(kGemvShapes[0], 0, z, z));
+        emit(gemv_dp4a_row(kGemvShapes[0], 0, runs, z, z));
+        emit(gemm_row(kGemmShapes[0], kGemmMs[0], 0, 0.0, runs, kVariants[0], z, z, z));
+        printf("\n]\n");
+        return 0;
+    }
+    hipStream_t s;
+    CHECK(hipStreamCreate(&s));
+    int rc;
+    if (op == "gemv") rc = run_gemv(false, runs, s);
+    else if (op == "gemv_dp4a") rc = run_gemv(true, runs, s);
+    else if (op == "gemm_wmma") rc = run_gemm(runs, s);
+    else {
+        fprintf(stderr, "unknown --op %s\n", op.c_str());
+        return 2;
+    }
+    printf(g_first ? "[\n]\n" : "\n]\n");
+    CHECK(hipStreamDestroy(s));
+    return rc;
+}

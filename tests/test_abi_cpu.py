@@ -57,7 +57,9 @@ def test_can_handle_gates(L, pkg):
     # the config shapes the reference's whitelist (patch:274-277) refused are served
     for K, N in [(5120, 8192), (5120, 1024), (8192, 5120), (5120, 17408), (17408, 5120), (4096, 4096)]:
         assert g(K, N, 1, T) and m(K, N, 512, T)
-    assert g(5120, 8192, 8, T) and not g(5120, 8192, 9, T)
+    # the GEMV dispatch has no M argument: one column only, as the reference's gate (patch:274-277)
+    assert g(5120, 8192, 1, T) and not g(5120, 8192, 2, T) and not g(5120, 8192, 8, T)
+    assert not g(5120, 8192, 9, T) and m(5120, 8192, 2, T) and m(5120, 8192, 8, T)
     assert not g(5120, 8192, 1, T + 1) and not m(5120, 8192, 512, 0)
     assert not g(5000, 8192, 1, T) and not m(5000, 64, 16, T)   # K % 256 != 0
     assert not g(0, 8, 1, T) and not g(256, 0, 1, T) and not m(256, 8, 0, T)
@@ -123,3 +125,55 @@ def test_product_package_has_no_oracle_dependency():
                 assert "oracle" not in text.replace("oracle is", ""), os.path.join(dirpath, f)
     out = subprocess.run(["ldd", os.path.join(pkg_dir, "libiq4xs_mi355x.so")], capture_output=True, text=True)
     assert "oracle" not in out.stdout
+
+
+REFERENCE_CPP_API = {  # the reference's own C++ signatures (include/iq4xs_reference_api.hpp cites each)
+    "quantize_row_q8_1_gpu(float const*, block_q8_1_real*, long, ihipStream_t*)",
+    "quantize_row_q8_1_batched_gpu(float const*, block_q8_1_real*, long, long, ihipStream_t*)",
+    "gemv_iq4xs_stock_dp4a_gpu(block_iq4_xs const*, float const*, float*, long, long, ihipStream_t*)",
+    "gemm_iq4xs_stock_dp4a_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "gemv_iq4xs_dp4a_gfx1100_prequantized_gpu(block_iq4_xs const*, block_q8_1_coop const*, float*, long, long, "
+    "ihipStream_t*)",
+    "gemv_iq4xs_dp4a_gfx1100_gpu(block_iq4_xs const*, float const*, float*, long, long, ihipStream_t*)",
+    "gemv_iq4xs_stock_gpu(block_iq4_xs const*, float const*, float*, long, long, ihipStream_t*)",
+    "gemm_iq4xs_stock_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "gemv_iq4xs_gfx1100_gpu(block_iq4_xs const*, float const*, float*, long, long, ihipStream_t*)",
+    "gemm_iq4xs_wmma_stream_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "gemm_iq4xs_wmma_p4_xor_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "gemm_iq4xs_wmma_64x64_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "gemm_iq4xs_stream_tiled_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "gemm_iq4xs_wmma_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "gemm_iq4xs_tiled_gpu(block_iq4_xs const*, float const*, float*, long, long, long, ihipStream_t*)",
+    "dequant_iq4xs_gpu(block_iq4_xs const*, float*, long, int, ihipStream_t*)",
+}
+# _Float16 in the LUT entry's signature: its mangled name, which binutils' demangler may not expand
+LUT_MANGLED = "_Z18gemm_iq4xs_lut_gpuPK12block_iq4_xsPKDF16_PKfPflllP12ihipStream_t"
+
+
+def test_library_exports_the_reference_cpp_api(L):
+    """The reference's tests and benches forward-declare these mangled names
+    (test_real_stock_compare.cpp:12-13, bench_gemm_wmma.cpp:23-28): the library
+    defines each with exactly that signature, so they link unchanged."""
+    out = subprocess.run(["nm", "-DC", "--defined-only", L.path], capture_output=True, text=True, check=True).stdout
+    defined = {line.split(" ", 2)[2] for line in out.splitlines() if " T " in line}
+    missing = sorted(REFERENCE_CPP_API - defined)
+    assert not missing, missing
+    raw = subprocess.run(["nm", "-D", "--defined-only", L.path], capture_output=True, text=True, check=True).stdout
+    assert LUT_MANGLED in raw or any(s.startswith("gemm_iq4xs_lut_gpu(block_iq4_xs const*, _Float16 const*")
+                                     for s in defined)
+
+
+def test_cpp_boundary_binary_links_the_reference_names():
+    """tests/cpp/boundary_test (built by __graft_entry__.build()) calls the hooks through
+    include/iq4xs_ggml_custom.cuh and the standalone API through the reference's own
+    declarations: the only library symbols it needs are the C hooks and those C++ names."""
+    binary = os.path.join(ROOT, "tests", "cpp", "_build", "boundary_test")
+    if not os.path.exists(binary):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "tests", "cpp")], check=True)
+    out = subprocess.run(["nm", "-C", "--undefined-only", binary], capture_output=True, text=True, check=True).stdout
+    und = {line.split(" U ", 1)[1].strip() for line in out.splitlines() if " U " in line}
+    for hook in ("custom_gemv_iq4xs_can_handle", "custom_gemv_iq4xs_dispatch", "custom_gemm_iq4xs_can_handle",
+                 "custom_gemm_iq4xs_dispatch"):
+        assert hook in und, hook
+    called = {s for s in und if "block_iq4_xs" in s or "block_q8_1_real" in s}
+    assert called and called <= REFERENCE_CPP_API | {s for s in und if s.startswith("_Z18gemm_iq4xs_lut_gpu")}, called

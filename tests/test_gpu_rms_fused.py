@@ -80,7 +80,36 @@ def test_fused_rejects(pkg, dev):
     # shapes the fused prologue does not take
     Ws = pkg.synthetic_weights(1024, N, seed=2, device=dev)
     assert f(1, P1(Ws.data_ptr()), yp, nn, X.data_ptr(), None, None, None, 1e-6, 1024, s) == nsup
-    Xb = torch.randn(16640, device=dev)
-    Wb = pkg.synthetic_weights(16640, N, seed=3, device=dev)
-    assert f(1, P1(Wb.data_ptr()), yp, nn, Xb.data_ptr(), None, None, None, 1e-6, 16640, s) == nsup
+    # past one pass-1 batch of the norm (K > 8192): the first K above the bound, the
+    # largest multiple of 256 that an earlier four-round batch took, and one beyond
+    for Kb in (8448, 16384, 16640):
+        Xb = torch.randn(Kb, device=dev)
+        Wb = pkg.synthetic_weights(Kb, N, seed=3, device=dev)
+        assert f(1, P1(Wb.data_ptr()), yp, nn, Xb.data_ptr(), None, None, None, 1e-6, Kb, s) == nsup, Kb
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("K", [8448, 16384])
+def test_two_call_path_past_fused_bound(pkg, orc, dev, K):
+    """Where the fused kernel refuses (K past one pass-1 batch), the two calls it
+    stands for -- the rms producer and the grouped GEMV -- still meet the oracle:
+    Q8_1 blocks and h bit for bit, outputs within the path's tolerance."""
+    from oracle.oracle import compute_metrics
+
+    print(f"rms two-call K={K}", flush=True)
+    N = 96
+    rng = np.random.default_rng(K)
+    x = (rng.standard_normal(K) * 3.0).astype(np.float32)
+    r = (rng.standard_normal(K) * 0.5).astype(np.float32)
+    gamma = (rng.random(K) + 0.5).astype(np.float32)
+    h_ref, _, blocks_ref = orc.rms_norm_q8_1(x, K, 1, R=r, gamma=gamma, eps=1e-6)
+    W = orc.gen_weights(K, N, seed=K + 1)
+    Xd, Rd, Gd = (torch.from_numpy(a).to(dev) for a in (x, r, gamma))
+    H = torch.empty(K, device=dev)
+    ws = pkg.rms_norm_q8_1(Xd, K, 1, residual=Rd, out_h=H, gamma=Gd, eps=1e-6)
+    (y,) = pkg.mul_mat_q8_1_group([torch.from_numpy(W).to(dev)], ws, K, [N], 1)
+    torch.cuda.synchronize()
+    assert np.array_equal(pkg.q8_1_blocks(ws, K, 1).cpu().numpy().ravel(), blocks_ref)
+    assert np.array_equal(H.cpu().numpy().view(np.uint32), h_ref.ravel().view(np.uint32))
+    m = compute_metrics(orc.gemv_semantics(W, blocks_ref, K, N), y.cpu().numpy().ravel())
+    assert m["rel_l2"] <= 1e-4 and not m["bad"], m
