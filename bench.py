@@ -507,7 +507,10 @@ def main() -> int:
     us_total = timer(next_step, args.steps)
     ms_per_step = us_total / args.steps / 1e3
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    step_stats = spread([timer(next_step, 1) / 1e3 for _ in range(args.repeats)], "ms_per_step")
+    # spread: each sample times one rotation of back-to-back steps (one step alone would
+    # also time the idle gap before its graph starts), divided by the steps in it
+    step_stats = spread([timer(next_step, args.layers) / args.layers / 1e3 for _ in range(args.repeats)],
+                        "ms_per_step")
 
     if args.copy_probe:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device=dev)

@@ -78,6 +78,9 @@ def test_harness_runs_on_gpu(op, want):
     for row in rows:
         d = dict(row)
         assert [k for k, _ in row] == OPS[want] and d["op"] == want
+        if d["winner"] == "SKIPPED":  # the LUT entry's shape gate (M < 512), reported as the reference does
+            assert d.get("variant") == "LUT_mu4" and d["M"] < 512, d
+            continue
         assert d["speedup"] > 0
         timed = [v for k, v in row if k.endswith("median_us")]
         assert timed and all(v > 0 for v in timed), d
