@@ -243,6 +243,22 @@ int iq4xs_mul_mat_q8_1_group(int count, const void* const* W, float* const* Y, c
 int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
                   size_t ws_bytes, void* stream);
 
+/* Largest Q8_1 workspace (iq4xs_workspace_bytes(K, M)) iq4xs_mul_mat_noalloc
+ * serves: 64 MiB, e.g. M <= 3400 at K = 17408, M <= 11600 at K = 5120. */
+#define IQ4XS_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* iq4xs_mul_mat without a workspace argument and without any allocation: the
+ * Q8_1 workspace is a static device array of IQ4XS_NOALLOC_SCRATCH_BYTES held
+ * by the library (one per GPU, for the life of the process).  No counterpart
+ * in the reference; for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same results
+ * as iq4xs_mul_mat bit for bit.  IQ4XS_ERROR_INVALID_VALUE when
+ * iq4xs_workspace_bytes(K, M) exceeds IQ4XS_NOALLOC_SCRATCH_BYTES.  Every call
+ * on one GPU shares that GPU's scratch: calls that overlap on one GPU (other
+ * streams, other host threads) race; serialise them. */
+int iq4xs_mul_mat_noalloc(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                          void* stream);
+
 /* Small-batch (1 <= M <= 8) multiply that quantises X to Q8_1 inside the GEMV
  * kernel (one launch, no workspace).  Same Q8_1 codes and sums as
  * iq4xs_quantize_q8_1 + iq4xs_mul_mat_q8_1.  Returns IQ4XS_ERROR_NOT_SUPPORTED

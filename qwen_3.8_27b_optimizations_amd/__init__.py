@@ -69,6 +69,7 @@ SIGNATURES = {
     "iq4xs_quantize_q8_1": (_INT, [_P, _I64, _I64, _INT, _P, ctypes.c_size_t, _P]),
     "iq4xs_mul_mat_q8_1": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _INT, _P]),
     "iq4xs_mul_mat": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, ctypes.c_size_t, _P]),
+    "iq4xs_mul_mat_noalloc": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "iq4xs_mul_mat_fused": (_INT, [_P, _P, _P, _I64, _I64, _I64, _INT, _P, _P]),
     "iq4xs_mul_mat_q8_1_group": (_INT, [_INT, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
     "iq4xs_rms_norm_q8_1": (_INT, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, _P, ctypes.c_size_t, _P]),

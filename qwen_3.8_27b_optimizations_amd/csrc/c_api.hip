@@ -13,6 +13,10 @@
 
 using namespace iq4xs;
 
+// The static device scratch of iq4xs_mul_mat_noalloc (its host-side lookup is
+// noalloc_scratch below).
+static __device__ __align__(256) uint8_t scratch[(size_t)IQ4XS_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
@@ -56,6 +60,34 @@ hipError_t pool_alloc(void** p, size_t bytes, hipStream_t stream) {
     });
     if (g_pool_err[dev] != hipSuccess) return g_pool_err[dev];
     return hipMallocFromPoolAsync(p, bytes, g_pool[dev], stream);
+}
+
+// Q8_1 workspace of iq4xs_mul_mat_noalloc: a file-scope device array of a fixed
+// size.  Every GPU the library runs on holds its own copy until the process
+// ends.  In host code `scratch` names a host-side stand-in, not device memory:
+// its device address is looked up once per device (hipGetSymbolAddress, with
+// that device current) and only that address is ever passed to a kernel.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)IQ4XS_NOALLOC_SCRATCH_BYTES;
+
+std::once_flag g_scratch_once[MAX_DEVICES];
+void* g_scratch_ptr[MAX_DEVICES];
+hipError_t g_scratch_err[MAX_DEVICES];
+
+// The current device's copy of `scratch` (looked up on the first call on that device).
+hipError_t noalloc_scratch(void** ptr) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::call_once(g_scratch_once[dev], [dev]() {
+        void* p = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+    });
+    if (g_scratch_err[dev] != hipSuccess) return g_scratch_err[dev];
+    if (g_scratch_ptr[dev] == nullptr) return hipErrorInvalidSymbol;
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
 }
 
 struct Planar {
@@ -305,6 +337,28 @@ int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N,
     if (err != hipSuccess) return err;
     return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, IQ4XS_PATH_AUTO, nullptr,
                           as_stream(stream));
+}
+
+// iq4xs_mul_mat with the Q8_1 workspace in the library's static device scratch:
+// no allocation of any kind.  Calls that overlap on one GPU share the scratch
+// and race; the quantiser rewrites every byte a multiply reads, so nothing is
+// cleared between calls.
+int iq4xs_mul_mat_noalloc(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
+                          void* stream) {
+    if (!valid_mat(W, X, Y, K, N, M) || (layout != LAYOUT_KM && layout != LAYOUT_MK)) return hipErrorInvalidValue;
+    if (planar_bytes(K, M) > NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;  // beyond the static scratch
+    void* ws = nullptr;
+    hipError_t err = noalloc_scratch(&ws);
+    if (err != hipSuccess) return err;
+    hipStream_t s = as_stream(stream);
+    if (prefer_fused(K, M)) {
+        const hipError_t e = mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, nullptr, s);
+        if (e != hipErrorNotSupported) return e;
+    }
+    const Planar p = planar_view(ws, K, M);
+    err = launch_quantize(X, K, M, layout, p.qs, p.ds, nullptr, s);
+    if (err != hipSuccess) return err;
+    return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, IQ4XS_PATH_AUTO, nullptr, s);
 }
 
 int iq4xs_mul_mat_fused(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
