@@ -171,7 +171,10 @@ int custom_gemm_iq4xs_dispatch(const void* W, const float* X, float* Y, int64_t 
  * real_stock_dp4a_comparator.hip:491,501).  For callers that own their memory:
  * the calls below allocate nothing and never synchronise.  The workspace holds
  * Q8_1 activations in planar form: int8 codes [M][K] at offset 0, then the
- * uint32 ds words [M][K/32] at a 256-byte aligned offset. */
+ * uint32 ds words [M][K/32], then the same codes as fp16 pairs [M][K/32][16]
+ * (uint32 word p of a 32-element block = elements p and p + 16), each part at
+ * a 256-byte aligned offset: 3 * K * M + K * M / 8 bytes and padding.  Every
+ * call that writes a workspace fills all three parts. */
 
 /* Bytes of workspace for M activation columns of length K. */
 size_t iq4xs_workspace_bytes(int64_t K, int64_t M);
@@ -244,8 +247,8 @@ int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N,
                   size_t ws_bytes, void* stream);
 
 /* Largest Q8_1 workspace (iq4xs_workspace_bytes(K, M)) iq4xs_mul_mat_noalloc
- * serves: 64 MiB, e.g. M <= 3400 at K = 17408, M <= 11600 at K = 5120. */
-#define IQ4XS_NOALLOC_SCRATCH_BYTES (64u << 20)
+ * serves: 128 MiB, e.g. M <= 2460 at K = 17408, M <= 8380 at K = 5120. */
+#define IQ4XS_NOALLOC_SCRATCH_BYTES (128u << 20)
 
 /* iq4xs_mul_mat without a workspace argument and without any allocation: the
  * Q8_1 workspace is a static device array of IQ4XS_NOALLOC_SCRATCH_BYTES held

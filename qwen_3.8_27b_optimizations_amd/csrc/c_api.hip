@@ -93,11 +93,13 @@ hipError_t noalloc_scratch(void** ptr) {
 struct Planar {
     int8_t* qs;
     uint32_t* ds;
+    uint32_t* hq;
 };
 
 Planar planar_view(const void* ws, int64_t K, int64_t M) {
     uint8_t* base = static_cast<uint8_t*>(const_cast<void*>(ws));
-    return {reinterpret_cast<int8_t*>(base), reinterpret_cast<uint32_t*>(base + planar_ds_offset(K, M))};
+    return {reinterpret_cast<int8_t*>(base), reinterpret_cast<uint32_t*>(base + planar_ds_offset(K, M)),
+            reinterpret_cast<uint32_t*>(base + planar_hq_offset(K, M))};
 }
 
 hipError_t mul_mat_planar(const uint8_t* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,
@@ -110,7 +112,7 @@ hipError_t mul_mat_planar(const uint8_t* W, const void* ws, float* Y, int64_t K,
         if (M > GEMV_MAX_COLS) return hipErrorInvalidValue;
         return launch_gemv(W, p.qs, p.ds, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
     }
-    if (path == IQ4XS_PATH_GEMM) return launch_gemm(W, p.qs, p.ds, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
+    if (path == IQ4XS_PATH_GEMM) return launch_gemm(W, p.qs, p.ds, p.hq, Y, K, N, M, ldy_m, ldy_n, dbg, stream);
     return hipErrorInvalidValue;
 }
 
@@ -153,7 +155,7 @@ hipError_t mul_mat_pooled(const void* W, const float* X, float* Y, int64_t K, in
     hipError_t err = pool_alloc(&ws, planar_bytes(K, M), stream);
     if (err != hipSuccess) return err;
     const Planar p = planar_view(ws, K, M);
-    err = launch_quantize(X, K, M, layout, p.qs, p.ds, nullptr, stream);
+    err = launch_quantize(X, K, M, layout, p.qs, p.ds, p.hq, nullptr, stream);
     if (err == hipSuccess)
         err = mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, IQ4XS_PATH_AUTO, nullptr,
                              stream);
@@ -167,12 +169,14 @@ extern "C" {
 
 int quantize_row_q8_1_gpu(const float* x, void* y, int64_t K, void* stream) {
     if (!x || !y || K <= 0 || K % QK8_1 != 0 || K >= MAX_DIM) return hipErrorInvalidValue;
-    return launch_quantize(x, K, 1, LAYOUT_MK, nullptr, nullptr, static_cast<block_q8_1*>(y), as_stream(stream));
+    return launch_quantize(x, K, 1, LAYOUT_MK, nullptr, nullptr, nullptr, static_cast<block_q8_1*>(y),
+                           as_stream(stream));
 }
 
 int quantize_row_q8_1_batched_gpu(const float* X, void* Y, int64_t K, int64_t M, void* stream) {
     if (!X || !Y || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
-    return launch_quantize(X, K, M, LAYOUT_KM, nullptr, nullptr, static_cast<block_q8_1*>(Y), as_stream(stream));
+    return launch_quantize(X, K, M, LAYOUT_KM, nullptr, nullptr, nullptr, static_cast<block_q8_1*>(Y),
+                           as_stream(stream));
 }
 
 int gemv_iq4xs_stock_dp4a_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream) {
@@ -195,7 +199,7 @@ int gemv_iq4xs_dp4a_gfx1100_prequantized_gpu(const void* W, const void* AQ, floa
     hipError_t err = pool_alloc(&ws, planar_bytes(K, 1), s);
     if (err != hipSuccess) return err;
     const Planar p = planar_view(ws, K, 1);
-    err = launch_coop_to_planar(static_cast<const uint8_t*>(AQ), K / QK8_1, p.qs, p.ds, s);
+    err = launch_coop_to_planar(static_cast<const uint8_t*>(AQ), K / QK8_1, p.qs, p.ds, p.hq, s);
     if (err == hipSuccess)
         err = mul_mat_planar(static_cast<const uint8_t*>(W), ws, y, K, N, 1, LAYOUT_MK, IQ4XS_PATH_AUTO, nullptr, s);
     const hipError_t ferr = hipFreeAsync(ws, s);
@@ -298,7 +302,7 @@ int iq4xs_quantize_q8_1(const float* X, int64_t K, int64_t M, int layout, void* 
     if ((layout != LAYOUT_KM && layout != LAYOUT_MK) || ws_bytes < planar_bytes(K, M)) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
     const Planar p = planar_view(ws, K, M);
-    return launch_quantize(X, K, M, layout, p.qs, p.ds, nullptr, as_stream(stream));
+    return launch_quantize(X, K, M, layout, p.qs, p.ds, p.hq, nullptr, as_stream(stream));
 }
 
 int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,
@@ -319,7 +323,7 @@ int iq4xs_mul_mat_q8_1_group(int count, const void* const* W, float* const* Y, c
     const uint8_t* Wb[GEMV_GROUP_MAX];
     for (int i = 0; i < count; ++i) Wb[i] = static_cast<const uint8_t*>(W[i]);
     if (M > GEMV_MAX_COLS)  // one GEMM launch: small matrices fill the big ones' last round
-        return launch_gemm_group(count, Wb, Y, N, p.qs, p.ds, K, M, layout == LAYOUT_MK, as_stream(stream));
+        return launch_gemm_group(count, Wb, Y, N, p.qs, p.ds, p.hq, K, M, layout == LAYOUT_MK, as_stream(stream));
     return launch_gemv_group(count, Wb, Y, N, p.qs, p.ds, K, M, layout == LAYOUT_MK, as_stream(stream));
 }
 
@@ -356,7 +360,7 @@ int iq4xs_mul_mat_noalloc(const void* W, const float* X, float* Y, int64_t K, in
         if (e != hipErrorNotSupported) return e;
     }
     const Planar p = planar_view(ws, K, M);
-    err = launch_quantize(X, K, M, layout, p.qs, p.ds, nullptr, s);
+    err = launch_quantize(X, K, M, layout, p.qs, p.ds, p.hq, nullptr, s);
     if (err != hipSuccess) return err;
     return mul_mat_planar(static_cast<const uint8_t*>(W), ws, Y, K, N, M, layout, IQ4XS_PATH_AUTO, nullptr, s);
 }
@@ -390,7 +394,7 @@ int iq4xs_rms_norm_q8_1(const float* X, const float* R, float* H, const float* g
     if (overlaps(ws, wsb, X, bytes) || overlaps(ws, wsb, R, bytes) || overlaps(ws, wsb, H, bytes))
         return hipErrorInvalidValue;
     const Planar p = planar_view(ws, K, M);
-    return launch_rms_norm_q8_1(X, R, H, gamma, eps, K, M, p.qs, p.ds, as_stream(stream));
+    return launch_rms_norm_q8_1(X, R, H, gamma, eps, K, M, p.qs, p.ds, p.hq, as_stream(stream));
 }
 
 int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void* ws, size_t ws_bytes,
@@ -399,7 +403,7 @@ int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void
         return hipErrorInvalidValue;
     if (ws_bytes < planar_bytes(K, M) || reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
     const Planar p = planar_view(ws, K, M);
-    return launch_swiglu_q8_1(G, U, K, M, p.qs, p.ds, as_stream(stream));
+    return launch_swiglu_q8_1(G, U, K, M, p.qs, p.ds, p.hq, as_stream(stream));
 }
 
 int iq4xs_rms_norm_mul_mat_group(int count, const void* const* W, float* const* Y, const int64_t* N, const float* X,

@@ -96,15 +96,31 @@ __global__ __launch_bounds__(256) void gfx1100_fp64_kernel(const uint8_t* __rest
 }
 
 // 64-byte padded Q8_1 blocks (ds at byte 0, codes at 16..47;
-// impl_gemv_dp4a_gfx1100.hip:60-66) -> the planar workspace of one column.
+// impl_gemv_dp4a_gfx1100.hip:60-66) -> the planar workspace of one column
+// (codes, ds and fp16 code pairs).
 __global__ __launch_bounds__(256) void coop_to_planar_kernel(const uint8_t* __restrict__ coop, int64_t nb,
-                                                             int8_t* __restrict__ qs, uint32_t* __restrict__ ds) {
+                                                             int8_t* __restrict__ qs, uint32_t* __restrict__ ds,
+                                                             uint32_t* __restrict__ hq) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t b = t >> 1;
     if (b >= nb) return;
     const int half = (int)(t & 1);
     const uint8_t* src = coop + b * 64;
-    *reinterpret_cast<v4i*>(qs + b * QK8_1 + 16 * half) = *reinterpret_cast<const v4i*>(src + 16 + 16 * half);
+    const v4i lo = *reinterpret_cast<const v4i*>(src + 16);  // elements 0..15
+    const v4i hi = *reinterpret_cast<const v4i*>(src + 32);  // elements 16..31
+    *reinterpret_cast<v4i*>(qs + b * QK8_1 + 16 * half) = half ? hi : lo;
+    // this thread's 8 pair words: elements p, p + 16 for p = 8 * half .. + 7
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int p = 8 * half + i;
+        const int a = (int8_t)((uint32_t)lo[p >> 2] >> (8 * (p & 3)));
+        const int c = (int8_t)((uint32_t)hi[p >> 2] >> (8 * (p & 3)));
+        w[i] = codes_to_half2(a, c);
+    }
+    v4i* o = reinterpret_cast<v4i*>(hq + b * 16 + 8 * half);
+    o[0] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    o[1] = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
     if (half == 0) ds[b] = *reinterpret_cast<const uint32_t*>(src);
 }
 
@@ -132,11 +148,12 @@ hipError_t launch_gfx1100_fp64(const uint8_t* W, const float* x, float* y, int64
     return hipGetLastError();
 }
 
-hipError_t launch_coop_to_planar(const uint8_t* coop, int64_t nb, int8_t* qs, uint32_t* ds, hipStream_t stream) {
+hipError_t launch_coop_to_planar(const uint8_t* coop, int64_t nb, int8_t* qs, uint32_t* ds, uint32_t* hq,
+                                 hipStream_t stream) {
     clear_launch_error();
     dim3 g;
     if (grid_of(nb * 2, g) != hipSuccess) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(coop_to_planar_kernel, g, dim3(256), 0, stream, coop, nb, qs, ds);
+    hipLaunchKernelGGL(coop_to_planar_kernel, g, dim3(256), 0, stream, coop, nb, qs, ds, hq);
     return hipGetLastError();
 }
 

@@ -1,13 +1,23 @@
-// gemm.hip -- IQ4_XS x Q8_1 prefill GEMM on gfx950 int8 MFMA.
+// gemm.hip -- IQ4_XS x Q8_1 prefill GEMM on gfx950 matrix cores.
 //
 // Semantics: the reference GEMM (real_stock_dp4a_comparator.hip:374-443):
 //   Y[n,m] = sum_kb fp16(W.d) * fp16(ds[m,kb].d) * (float)(sumi[n,m,kb] * (ls-32))
 // where sumi is the exact int32 dot of a 32-weight sub-block with the
 // matching Q8_1 block.
 //
-// Two kernels share this scheme (the launcher picks one per shape):
-// gemm_iq4xs_db_kernel (128x128 tile, 16 waves, double-buffered LDS) and
-// gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves, three per CU).
+// Default kernel: gemm_f16_kernel (128x128 tile, 8 waves, two LDS stages),
+// which runs the integer products on v_mfma_f32_32x32x16_f16 -- codebook
+// values and Q8_1 codes are exact in fp16 and a sub-block's 32-term sum is an
+// integer below 2^24, so the MFMA returns sumi exactly, as a float -- and
+// leaves one FMA per output and sub-block for the epilogue.  Its design notes
+// are with the kernel below.
+//
+// The int8 kernels below it, gemm_iq4xs_db_kernel (128x128 tile, 16 waves,
+// double-buffered LDS) and gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves,
+// three per CU), run the products on v_mfma_i32_32x32x32_i8 and need a
+// convert as well as the FMA per output and sub-block; they serve K beyond
+// the fp16 kernel's 32-bit offsets and stay selectable for comparison
+// (IQ4XS_GEMM_KIND = 0 / 1 / -1).  Notes on them:
 //
 // Both are VALU-issue bound.  Every output needs its own scale per sub-block,
 // d_w[n] * d_x[m], so the epilogue costs VALU work per output and sub-block
@@ -26,10 +36,11 @@
 // multiplies; keeping (ls - 32) as int8 with d_w applied once per super-block
 // (exact int32 sumi*(ls-32)) was 4-8 % slower.
 //
-// Non-finite scales (an fp16 d of Inf/NaN) give NaN where the reference's
-// product would give +-Inf: the hi/lo split of an infinite scale is Inf + NaN.
+// Non-finite scales (an fp16 d of Inf/NaN) give NaN in the int8 kernels where
+// the reference's product would give +-Inf: the hi/lo split of an infinite
+// scale is Inf + NaN.  The fp16 kernel keeps the reference's +-Inf.
 //
-// MI355X mapping (64x64 kernel).  A workgroup (4 waves) owns a 64-row x
+// MI355X mapping (64x64 int8 kernel).  A workgroup (4 waves) owns a 64-row x
 // 64-token output tile and walks K one 256-weight super-block at a time:
 //   1. the 64 weight rows' super-blocks are decoded (v_perm codebook lookup,
 //      decode_codes_x)
@@ -427,12 +438,450 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const GemmGro
     }
 }
 
+// ---------------------------------------------------------------- fp16 matrix-core kernel
+// The IQ4_XS codebook values (-127..113) and the Q8_1 codes (-127..127) are
+// exact in fp16, and every partial sum of a 32-term dot of them is an integer
+// below 2^24, so two v_mfma_f32_32x32x16_f16 return the reference's int32 sumi
+// of a sub-block exactly, already as a float.  The epilogue is then one FMA
+// per output and sub-block, acc += sc * S, where the int8 MFMA path needs a
+// convert as well.  The scale tile sc = d_x * (d_w * (ls - 32)) comes from a
+// v_mfma_f32_32x32x16_bf16 on exact bf16 hi/lo halves of both factors.
+//
+// Workgroup: 8 waves, a 128-row x 128-token tile.  Wave w owns weight rows
+// 32 * (w & 3) .. + 31 against all 128 tokens (four 32x32 blocks) and the
+// sub-blocks 4 * (w >> 2) .. + 3 of every super-block; the two waves of a row
+// group share a SIMD and add their partial sums at the end (a fixed order,
+// whatever the grid).  The MFMA's A operand is the tokens, B the weights, so a
+// lane's 16 accumulators are one weight row (its own) against 16 tokens.
+//   * Weights: each lane loads its row's header and the 8 qs bytes its MFMA
+//     half needs from each of its 4 sub-blocks straight into registers, two
+//     super-blocks ahead of use; a qs byte becomes its fp16 code pair through
+//     a 256-word table in LDS (one SDWA shift for the address, one ds_read).
+//     The lane halves take the high and low bf16 half of the row's scale.
+//   * Tokens: the workspace's fp16 code pairs (word p = elements p, p + 16 of a
+//     block), copied by direct-to-LDS loads (global_load_lds_dwordx4, no
+//     VGPRs), two stages of a super-block each.  A token row is 512 bytes; its
+//     16-byte chunk c sits at c ^ (row & 15), so the 32 lanes of a fragment
+//     read hit distinct bank groups.  Word p of a block pairs elements p and
+//     p + 16, which is exactly the k order of the weight fragment: lane half h
+//     of MFMA u takes qs bytes 8h + 4u .. + 3, low and high nibble of each.
+//   * Token scales: bf16 hi/lo pairs of d_x, [token][sub-block], per stage.
+// Each wave runs its 16 (sub-block, token block) steps of a super-block as a
+// software pipeline: step t issues its three MFMAs, each followed by the LDS
+// read that refills its A operand for step t + 1 and by a share of the VALU
+// work (the FMAs of step t - 1, a third of the next sub-block's decode).
+// Measured on gfx950: a wave's VALU ops issue at about half rate while an
+// MFMA runs, so this design is bound by VALU issue (FMA, decode) plus half
+// the MFMA time; the time per step follows that sum.
+// Results are bit-identical for any grid: a row's arithmetic depends on K only.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// s_waitcnt vmcnt(5) (expcnt and lgkmcnt left at their maxima), gfx9 encoding
+constexpr int kVmcnt5 = 5 | (0x7 << 4) | (0xF << 8);
+
+constexpr int H_BN = 128, H_BM = 128, H_THREADS = 512;
+constexpr int H_ROW = 512;                           // LDS bytes per token row of a super-block
+constexpr int H_T_OFF = H_BM * H_ROW;                // token scale pairs, uint32 [128][8]
+constexpr int H_STAGE = H_T_OFF + H_BM * 8 * 4;      // 68 KB
+constexpr int H_LUT = 1024;                          // the code pair table
+// the table and two stages: 137 KB of gfx950's 160 KB of LDS per CU
+
+__device__ inline int h_chunk(int m, int c) { return m * H_ROW + ((c ^ (m & 15)) << 4); }
+
+// bf16 hi | lo << 16 with hi + lo == x exactly for finite x of at most 16
+// significant bits; a non-finite x keeps lo = 0, so that the scale product is
+// +-Inf (or NaN) exactly as the reference's product would be.
+__device__ inline uint32_t bf16_pair_f(float x) {
+    const uint32_t hb = __builtin_bit_cast(uint32_t, x) & 0xFFFF0000u;
+    const float lo = x - __builtin_bit_cast(float, hb);
+    const uint32_t lb = __builtin_isfinite(x) ? (__builtin_bit_cast(uint32_t, lo) & 0xFFFF0000u) : 0u;
+    return (hb >> 16) | lb;
+}
+
+// Four int8 codebook values of low nibbles (lo) and of high nibbles (hi) ->
+// four fp16 pair words {lo byte j, hi byte j}, exactly (v_cvt_f16_i16 on a
+// sign-extended byte, written to one half of the word: one op per value).
+__device__ inline v4u kv_pairs_f16(uint32_t lo, uint32_t hi) {
+    uint32_t r0, r1, r2, r3;
+    asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+        : "v"(lo), "v"(hi));
+    return v4u{r0, r1, r2, r3};
+}
+
+// The fp16 code pair word of a qs byte b, {kv[b & 15], kv[b >> 4]}: the
+// MFMA B operand's pair for the two weights that byte encodes (low nibble:
+// element p, high nibble: element p + 16 of the sub-block).  A 256-entry
+// table of these words sits at LDS address 0 of the fp16 kernel.
+__device__ inline uint32_t kv_pair_word(int b) {
+    const uint32_t kv[4] = {KV0, KV1, KV2, KV3};
+    const int lo = b & 15, hi = b >> 4;
+    return codes_to_half2((int8_t)(kv[lo >> 2] >> (8 * (lo & 3))), (int8_t)(kv[hi >> 2] >> (8 * (hi & 3))));
+}
+
+// The four qs bytes of q -> their four pair words, from the table at `lut`:
+// one v_lshlrev_b32_sdwa (byte k -> its word's byte offset) and one
+// ds_read_b32 per byte, against 19 VALU ops for the in-register decode.
+__device__ inline v4u lut_pairs(const uint8_t* lut, uint32_t q) {
+    uint32_t o0, o1, o2, o3;
+    asm("v_lshlrev_b32_sdwa %0, 2, %4 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+        "v_lshlrev_b32_sdwa %1, 2, %4 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+        "v_lshlrev_b32_sdwa %2, 2, %4 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+        "v_lshlrev_b32_sdwa %3, 2, %4 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=&v"(o0), "=&v"(o1), "=&v"(o2), "=&v"(o3)  // early clobber: q is read after o0 is written
+        : "v"(q));
+    return v4u{*reinterpret_cast<const uint32_t*>(lut + o0), *reinterpret_cast<const uint32_t*>(lut + o1),
+               *reinterpret_cast<const uint32_t*>(lut + o2), *reinterpret_cast<const uint32_t*>(lut + o3)};
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 32-bit LDS address of a __shared__ object.
+__device__ inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(lds_ptr_t)(const_cast<void*>(p));
+}
+
+// One 16-byte chunk per lane, global (sbase + voff) -> LDS at lds + 16 * lane
+// (lds wave-uniform, in M0).  Written as asm so that the compiler does not
+// treat it as an LDS store: it would otherwise make every later LDS read wait
+// for it, the next stage's copy included.  The kernel itself waits (vmcnt)
+// before the barrier that publishes the stage; the compiler's own loads stay
+// correct, since vmcnt retires in order and its waits can only over-wait.
+// Nothing else in the kernel uses M0.
+__device__ inline void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+}
+
+struct HWeights {  // one super-block of this lane's weight row: header, and qs bytes 8h..8h+7 of 4 sub-blocks
+    v2u hdr;
+    v2u qs[4];
+};
+
+// One super-block of the fp16 kernel for one wave: the MFMAs and epilogue of
+// its 4 sub-blocks x 4 token blocks from stage `st` (tokens) and `w` (its
+// weight row), as a software pipeline over the 16 (sub-block, token block)
+// steps: step t issues its three MFMAs, then the FMAs of step t - 1 (whose
+// results have landed meanwhile) while the LDS fragments of step t + 1 are in
+// flight; the next sub-block's weights are decoded during the current one.
+// `w` is reloaded with the next super-block (load_next) once its last
+// sub-block is decoded, so one set of weight registers serves both.
+template <bool kDebug, typename LoadNext>
+__device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t* lut, HWeights& w, v16f (&acc)[4],
+                                               int kh, int h, int col, int lane, int64_t kb, int64_t m0, int64_t M,
+                                               int64_t n, int64_t N, int64_t nb, int32_t* __restrict__ dbg,
+                                               LoadNext&& load_next) {
+    // this wave's half of the 6-bit scales at sub-block positions 0-3
+    const uint32_t h0 = (w.hdr.x & 0xFFFFu) | ((w.hdr.x >> (8 * kh)) & 0xFF0000u), h1 = w.hdr.y >> (16 * kh);
+    const float dw = half_bits_to_float(h0 & 0xFFFFu), dw_m32 = -32.0f * dw;
+    // lane half h = 1 takes the low bf16 half of each weight scale; for an
+    // infinite or NaN d_w that half is 0 (the high half carries the Inf/NaN)
+    const uint32_t hmask = h ? 0xFFFF0000u : 0u;
+    const bool zap = h && !__builtin_isfinite(dw);
+    // B operands of sub-block i, built in three parts spread over the steps
+    // of the previous sub-block: the fp16 codes (b0: k 0-15, b1: k 16-31 of
+    // the MFMA pair) and the scale column bsc: this row's d_w * (ls - 32)
+    // split into exact bf16 halves, the high half in lane half 0 and the low
+    // half in lane half 1, at k slots 2i, 2i + 1 of that half
+    auto decode = [&](int i, int part, v4u& b0, v4u& b1, v4u& bsc) {
+        if (part == 2) {
+            const uint32_t lsr = subblock_ls(h0, h1, i);  // ls + 32, 0..63
+            const float x = __builtin_fmaf(dw, (float)(int)lsr, dw_m32);  // exact: at most 16 significant bits
+            const uint32_t xb = __builtin_bit_cast(uint32_t, x);
+            uint32_t v = __builtin_bit_cast(uint32_t, x - __builtin_bit_cast(float, xb & hmask));
+            v = zap ? 0u : v;
+            bsc = v4u{0u, 0u, 0u, 0u};
+            bsc[i] = __builtin_amdgcn_perm(v, v, 0x07060706u);
+        } else {
+            (part ? b1 : b0) = lut_pairs(lut, part ? w.qs[i].y : w.qs[i].x);
+        }
+    };
+    // operand r of step t (token block j = t & 3, sub-block 4 kh + (t >> 2)):
+    // r = 0, 1: the A operands of the two code MFMAs; r = 2: the scale MFMA's
+    // A operand, the bf16 pairs of d_x of this wave's 4 sub-blocks for token
+    // 32 j + col
+    auto frag = [&](int t, int r, v4u& a) {
+        const int m = 32 * (t & 3) + col, s = 4 * kh + (t >> 2);
+        if (r < 2)
+            a = *reinterpret_cast<const v4u*>(st + h_chunk(m, 4 * s + 2 * h + r));
+        else
+            a = *reinterpret_cast<const v4u*>(st + H_T_OFF + m * 32 + 16 * kh);
+    };
+    // half q of the epilogue of step t: acc += sp * dp for accumulators 8q .. 8q + 7
+    auto epilogue = [&](int t, const v16f& dp, const v16f& sp, int q) {
+        const int jp = t & 3;
+#pragma unroll
+        for (int e = 8 * q; e < 8 * q + 8; ++e) {
+            acc[jp][e] = __builtin_fmaf(sp[e], dp[e], acc[jp][e]);
+            if (kDebug) {
+                const int s = 4 * kh + (t >> 2);
+                const int64_t mg = m0 + 32 * jp + mfma_c_row(e, lane);
+                if (mg < M && n < N)
+                    dbg[(mg * N + n) * nb + kb * 8 + s] = (int)dp[e] * (subblock_ls(h0, h1, t >> 2) - 32);
+            }
+        }
+        // pin the epilogue here: without it the optimiser sinks every FMA to
+        // the end of the super-block and spills the MFMA results
+        asm volatile("" : "+v"(acc[jp]));
+    };
+
+    v4u b0, b1, bsc, nb0, nb1, nbsc, a0, a1, ts;
+#pragma unroll
+    for (int part = 0; part < 3; ++part) decode(0, part, b0, b1, bsc);
+    frag(0, 0, a0);
+    frag(0, 1, a1);
+    frag(0, 2, ts);
+    v16f dp, sp;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int i = t >> 2, j = t & 3;
+        // each MFMA is followed by the LDS read that refills its A operand for
+        // step t + 1 and by a share of the VALU work (the FMAs of step t - 1,
+        // then a part of the next sub-block's decode), so that the wave issues
+        // VALU ops while its MFMAs run instead of stalling on a busy matrix
+        // pipe; the scheduling barriers keep that order
+        v16f d = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a0), __builtin_bit_cast(v8h, b0),
+                                                        v16f{}, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 1 < 16) frag(t + 1, 0, a0);
+        if (t > 0) epilogue(t - 1, dp, sp, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        d = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a1), __builtin_bit_cast(v8h, b1), d, 0, 0,
+                                                   0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 1 < 16) frag(t + 1, 1, a1);
+        if (t > 0) epilogue(t - 1, dp, sp, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ts),
+                                                                __builtin_bit_cast(v8bf, bsc), v16f{}, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 1 < 16) frag(t + 1, 2, ts);
+        if (i < 3 && j < 3) decode(i + 1, j, nb0, nb1, nbsc);
+        if (i < 3 && j == 3) {
+            b0 = nb0;
+            b1 = nb1;
+            bsc = nbsc;
+        }
+        if (t == 10) load_next(w);  // decode(3) in steps 8-10 was the last use of w
+        dp = d;
+        sp = sc;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    epilogue(15, dp, sp, 0);
+    epilogue(15, dp, sp, 1);
+}
+
+template <bool kDebug, bool kGroup>
+__global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp, const uint32_t* __restrict__ ahq,
+                                                             const uint32_t* __restrict__ ads, int64_t K, int64_t M,
+                                                             int64_t ldy_n, int tiles_x, int tiles,
+                                                             int32_t* __restrict__ dbg) {
+    // LDS: the 1 KB code pair table at address 0, then the two stages
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[H_LUT + 2 * H_STAGE];
+    uint8_t(*const stages)[H_STAGE] = reinterpret_cast<uint8_t(*)[H_STAGE]>(smem + H_LUT);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
+    const int rg = wave & 3, kh = wave >> 2, h = lane >> 5, col = lane & 31;
+
+    // XCD-aware tile order: the 8 XCDs take workgroups round-robin, so
+    // workgroup b runs on XCD b % 8; each XCD is given a contiguous range of
+    // the token-major tile order, so its tiles share few token tiles (L2).
+    int tile;
+    {
+        const int b = (int)blockIdx.x, x = b & 7, q = tiles >> 3, r = tiles & 7;
+        tile = x * q + min(x, r) + (b >> 3);
+    }
+    const int bx = tile % tiles_x, by = tile / tiles_x;
+    // the matrix of this tile: gemm_select's choice, by the logical tile index
+    const uint8_t* W = grp.W[0];
+    float* Y = grp.Y[0];
+    int64_t N = grp.N[0], ldy_m = grp.ldy_m[0];
+    int tile0 = 0;
+    if (kGroup) {
+        int gsel = 0;
+#pragma unroll
+        for (int i = 0; i + 1 < GEMV_GROUP_MAX; ++i) gsel += bx >= grp.tile_end[i] ? 1 : 0;
+#pragma unroll
+        for (int i = 1; i < GEMV_GROUP_MAX; ++i) {
+            if (gsel == i) {
+                W = grp.W[i];
+                Y = grp.Y[i];
+                N = grp.N[i];
+                ldy_m = grp.ldy_m[i];
+                tile0 = grp.tile_end[i - 1];
+            }
+        }
+    }
+    const int64_t n0 = (int64_t)(bx - tile0) * H_BN;
+    const int64_t m0 = (int64_t)by * H_BM;
+    const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
+
+    // ---- this lane's weight row (rows past N repeat the last; never stored)
+    const int64_t n = n0 + 32 * rg + col;
+    const uint8_t* wtile = W + n0 * row_bytes;
+    const uint32_t woff = (uint32_t)(((n < N) ? n - n0 : N - 1 - n0) * row_bytes);
+    auto load_w = [&](HWeights& g, int64_t kb) {
+        const uint8_t* p = wtile + kb * BLOCK_BYTES + woff;
+        g.hdr = *reinterpret_cast<const v2u*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) g.qs[i] = *reinterpret_cast<const v2u*>(p + 8 + 16 * (4 * kh + i) + 8 * h);
+    };
+
+    // ---- token staging: instruction i of this wave fills LDS chunks
+    // (wave * 8 + i) * 64 + lane of a stage (token row chunk >> 5, chunk & 31)
+    // (16 * wave + 2 * i + h, chunk col ^ (2 i + h) of that row: the swizzle)
+    const uint8_t* xtile = reinterpret_cast<const uint8_t*>(ahq) + m0 * (2 * K);
+    const int xrow = 16 * wave + h, xlast = (int)min<int64_t>(M - 1 - m0, H_BM - 1);  // rows past M repeat the last
+    const uint32_t xstride = (uint32_t)(2 * K), xcol = 16u * (uint32_t)(col ^ h);
+    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_addr(&stages[0][0]) + wave * 8 * 1024);
+    auto issue_x = [&](int64_t kb, int stage) {
+        const uint8_t* src = xtile + kb * 512;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t voff = (uint32_t)min(xrow + 2 * i, xlast) * xstride + (xcol ^ (32u * i));
+            dma16(src, voff, lds_wave + stage * H_STAGE + i * 1024);
+        }
+    };
+    // token scales: thread tid -> token tid >> 2, sub-blocks 2 (tid & 3), + 1
+    const int tm = tid >> 2, ts = 2 * (tid & 3);
+    const uint32_t* dtile = ads + m0 * nb;
+    const uint32_t doff = (uint32_t)(((m0 + tm < M) ? tm : M - 1 - m0) * nb + ts);
+    auto load_d = [&](int64_t kb) { return *reinterpret_cast<const v2u*>(dtile + kb * 8 + doff); };
+    auto store_d = [&](v2u d, uint8_t* stage) {
+        uint32_t* t = reinterpret_cast<uint32_t*>(stage + H_T_OFF) + tm * 8 + ts;
+        *reinterpret_cast<v2u*>(t) = v2u{bf16_pair_f(half_bits_to_float(d.x & 0xFFFFu)),
+                                         bf16_pair_f(half_bits_to_float(d.y & 0xFFFFu))};
+    };
+
+    v16f acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = v16f{};
+
+    // weights run two super-blocks ahead: w holds super-block kb, wn kb + 1,
+    // and kb + 2 is loaded into w's registers once kb's decode is done
+    if (tid < 256) reinterpret_cast<uint32_t*>(smem)[tid] = kv_pair_word(tid);  // published by the barrier below
+
+    HWeights w, wn;
+    load_w(w, 0);
+    if (bpr > 1) load_w(wn, 1);
+    issue_x(0, 0);
+    {
+        const v2u d0 = load_d(0);
+        __builtin_amdgcn_s_waitcnt(0);
+        store_d(d0, stages[0]);
+    }
+    __syncthreads();
+
+    // one super-block from stage kb & 1 while super-block kb + 1 streams into
+    // the other; wc holds kb's weights, wo kb + 1's
+    // The loads are issued unconditionally (past the end they repeat the last
+    // super-block into registers and a stage that nothing reads any more), so
+    // that every iteration issues the same sequence: 8 copies + 1 token-scale
+    // load at the start, 5 weight loads at step 10; the wait before the
+    // barrier then leaves exactly the 5 weight loads in flight.
+    auto superblock = [&](int64_t kb, HWeights& wc) {
+        const int cur = (int)(kb & 1);
+        const int64_t kb1 = min(kb + 1, bpr - 1), kb2 = min(kb + 2, bpr - 1);
+        issue_x(kb1, cur ^ 1);
+        v2u dnext = load_d(kb1);
+        f16_superblock<kDebug>(stages[cur], smem, wc, acc, kh, h, col, lane, kb, m0, M, n, N, nb, dbg,
+                               [&](HWeights& g) { load_w(g, kb2); });
+        // this thread's direct-to-LDS copies and token scales have landed; the
+        // 5 weight loads of super-block kb + 2, issued after them, may still
+        // be in flight (vmcnt counts completions in issue order)
+        __builtin_amdgcn_s_waitcnt(kVmcnt5);
+        // keep the conversion of the token scales here: hoisted next to their
+        // load it would need a vmcnt(0) there, i.e. wait for the whole next
+        // stage before computing this one
+        asm volatile("" : "+v"(dnext));
+        if (kb + 1 < bpr) store_d(dnext, stages[cur ^ 1]);
+        __syncthreads();
+    };
+    // two super-blocks per iteration, so that the weight registers swap
+    // roles without copies (a copy of a register still being loaded would
+    // have to wait for the load)
+    // (an odd last super-block is peeled off, so that the loop is always
+    // entered from the second half: the compiler's own waits then know which
+    // weight loads are still in flight)
+    int64_t kb = 0;
+    for (; kb + 1 < bpr; kb += 2) {
+        superblock(kb, w);
+        superblock(kb + 1, wn);
+    }
+    if (kb < bpr) superblock(kb, w);
+
+    // the two sub-block halves of each row group add their partial sums: kh = 1
+    // hands blocks 0, 1 to kh = 0 and takes blocks 2, 3 (constant indices only:
+    // a runtime index into acc would put it in scratch memory)
+    float* red = reinterpret_cast<float*>(&stages[0][0]);  // both stages are free now
+    auto put = [&](const v16f& a, int slot) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[((rg * 2 + kh) * 2 + slot) * 1024 + e * 64 + lane] = a[e];
+    };
+    auto take = [&](v16f& a, int slot) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) a[e] += red[((rg * 2 + (kh ^ 1)) * 2 + slot) * 1024 + e * 64 + lane];
+    };
+    auto store = [&](const v16f& a, int j) {
+        if (n >= N) return;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t mg = m0 + 32 * j + mfma_c_row(e, lane);
+            if (mg < M) Y[mg * ldy_m + n * ldy_n] = a[e];
+        }
+    };
+    if (kh) {
+        put(acc[0], 0);
+        put(acc[1], 1);
+    } else {
+        put(acc[2], 0);
+        put(acc[3], 1);
+    }
+    __syncthreads();
+    if (kh) {
+        take(acc[2], 0);
+        take(acc[3], 1);
+        store(acc[2], 2);
+        store(acc[3], 3);
+    } else {
+        take(acc[0], 0);
+        take(acc[1], 1);
+        store(acc[0], 0);
+        store(acc[1], 1);
+    }
+}
+
 static int gemm_kind() {
     static const int kind = []() {
-        const char* v = getenv("IQ4XS_GEMM_KIND");  // tuning override: 0 = 64x64, 1 = 128x128
-        return v ? atoi(v) : -1;
+        const char* v = getenv("IQ4XS_GEMM_KIND");  // tuning override: 0 = 64x64, 1 = 128x128, 2 = fp16 matrix cores
+        return v ? atoi(v) : 2;
     }();
     return kind;
+}
+
+template <bool kDebug, bool kGroup>
+static hipError_t launch_f16_kernel(const GemmGroup& grp, int64_t tiles_x, const uint32_t* ahq, const uint32_t* ads,
+                                    int64_t K, int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    const int64_t tiles_y = (M + H_BM - 1) / H_BM;
+    const int64_t tiles = tiles_x * tiles_y;
+    if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((gemm_f16_kernel<kDebug, kGroup>), dim3((unsigned)tiles), dim3(H_THREADS), 0, stream, grp, ahq,
+                       ads, K, M, ldy_n, (int)tiles_x, (int)tiles, dbg);
+    return hipGetLastError();
+}
+
+// The fp16 kernel addresses a tile's weight rows and tokens with 32-bit offsets.
+static bool f16_fits(int64_t K) {
+    return (int64_t)H_BN * (K / QK_K) * BLOCK_BYTES < (1ll << 32) && (int64_t)H_BM * 2 * K < (1ll << 32);
 }
 
 // The 128x128 kernel runs one workgroup per CU and is faster per tile; the
@@ -473,9 +922,22 @@ static hipError_t launch_gemm_kernel(bool big, const GemmGroup& grp, int64_t gx,
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
-                       int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const uint32_t* ahq, float* Y,
+                       int64_t K, int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
+                       hipStream_t stream) {
     clear_launch_error();
+    if (gemm_kind() == 2 && f16_fits(K)) {
+        GemmGroup grp{};
+        grp.W[0] = W;
+        grp.Y[0] = Y;
+        grp.N[0] = N;
+        grp.ldy_m[0] = ldy_m;
+        const int64_t gx = (N + H_BN - 1) / H_BN;
+        if (gx > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        grp.tile_end[0] = (int)gx;
+        return dbg ? launch_f16_kernel<true, false>(grp, gx, ahq, ads, K, M, ldy_n, dbg, stream)
+                   : launch_f16_kernel<false, false>(grp, gx, ahq, ads, K, M, ldy_n, dbg, stream);
+    }
     const bool big = use_big_tiles(N, M, K);
     GemmGroup grp{};
     grp.W[0] = W;
@@ -520,11 +982,27 @@ hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads,
 // summed rows, so the small matrices fill CUs that the big ones' last round
 // leaves idle.
 hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N, const int8_t* aqs,
-                             const uint32_t* ads, int64_t K, int64_t M, bool layout_mk, hipStream_t stream) {
+                             const uint32_t* ads, const uint32_t* ahq, int64_t K, int64_t M, bool layout_mk,
+                             hipStream_t stream) {
     clear_launch_error();
     if (count < 1 || count > GEMV_GROUP_MAX) return hipErrorInvalidValue;
     int64_t n_sum = 0;
     for (int i = 0; i < count; ++i) n_sum += N[i];
+    if (gemm_kind() == 2 && f16_fits(K)) {
+        GemmGroup grp{};
+        int64_t tiles = 0;
+        for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
+            const int j = i < count ? i : count - 1;  // unused entries repeat the last matrix, past every tile
+            if (i < count) tiles += (N[j] + H_BN - 1) / H_BN;
+            if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+            grp.W[i] = W[j];
+            grp.Y[i] = Y[j];
+            grp.N[i] = N[j];
+            grp.ldy_m[i] = layout_mk ? N[j] : 1;
+            grp.tile_end[i] = (int)tiles;
+        }
+        return launch_f16_kernel<false, true>(grp, tiles, ahq, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
+    }
     const bool big = use_big_tiles(n_sum, M, K);
     const int bn = big ? G2_BN : GEMM_BN;
     GemmGroup grp{};

@@ -47,8 +47,20 @@ typedef int v4i_a8 __attribute__((ext_vector_type(4), aligned(8)));
 __host__ __device__ inline size_t planar_ds_offset(int64_t K, int64_t M) {
     return ((size_t)(K * M) + 255u) & ~(size_t)255u;
 }
+// The same codes as fp16 values (exact: |q| <= 127), for the matrix-core GEMM:
+// hq [M][K/32][16] uint32 at the next 256-byte boundary, word p of a block
+// holding the fp16 codes of elements p (low half) and p + 16 (high half).
+__host__ __device__ inline size_t planar_hq_offset(int64_t K, int64_t M) {
+    return (planar_ds_offset(K, M) + (size_t)M * (size_t)(K / QK8_1) * 4u + 255u) & ~(size_t)255u;
+}
 __host__ __device__ inline size_t planar_bytes(int64_t K, int64_t M) {
-    return planar_ds_offset(K, M) + (size_t)M * (size_t)(K / QK8_1) * 4u;
+    return planar_hq_offset(K, M) + (size_t)M * (size_t)K * 2u;
+}
+
+// Two int8 codes as an fp16 pair word (lo | hi << 16), exactly.
+__device__ inline uint32_t codes_to_half2(int lo, int hi) {
+    const _Float16 a = (_Float16)(short)lo, b = (_Float16)(short)hi;
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
 // Exact binary16 -> binary32 (hardware conversion; fp16 denormals are kept).

@@ -24,7 +24,8 @@ constexpr int LAYOUT_MK = 1;  // X[m*K+k], Y[m*N+n]   (ggml src1 / dst)
 // MFMA GEMM.
 constexpr int GEMV_MAX_COLS = 8;
 
-hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds,
+// Planar writers fill all three parts (qs, ds, hq) when qs is non-null.
+hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds, uint32_t* hq,
                            block_q8_1* blocks, hipStream_t stream);
 hipError_t launch_planar_to_blocks(const int8_t* qs, const uint32_t* ds, int64_t K, int64_t M, block_q8_1* blocks,
                                    hipStream_t stream);
@@ -64,14 +65,17 @@ hipError_t launch_gemv_rms_group(int count, const uint8_t* const* W, float* cons
                                  const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
                                  hipStream_t stream);
 
-// Same contract on the int8 MFMA path (any M >= 1).
-hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
-                       int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
+// Same contract on the matrix-core GEMM path (any M >= 1); it also reads the
+// workspace's fp16 code pairs ahq.
+hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const uint32_t* ahq, float* Y,
+                       int64_t K, int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
+                       hipStream_t stream);
 
 // Y[i] = W[i] x for i < count <= GEMV_GROUP_MAX on the int8 MFMA path, one
 // launch; Y[i] is [M][N[i]] (layout_mk) or [N[i]][M].
 hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N, const int8_t* aqs,
-                             const uint32_t* ads, int64_t K, int64_t M, bool layout_mk, hipStream_t stream);
+                             const uint32_t* ads, const uint32_t* ahq, int64_t K, int64_t M, bool layout_mk,
+                             hipStream_t stream);
 
 // One v_mfma_i32_32x32x32_i8 on A[32][32], B[32][32] (k-contiguous rows) ->
 // C[32][32] = A B^T, through the operand layouts the GEMM uses.
@@ -86,15 +90,16 @@ hipError_t launch_dequant(const uint8_t* src, float* dst, int64_t n_blocks, hipS
 hipError_t launch_stock_fp64(const uint8_t* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
                              hipStream_t stream);
 hipError_t launch_gfx1100_fp64(const uint8_t* W, const float* x, float* y, int64_t K, int64_t N, hipStream_t stream);
-hipError_t launch_coop_to_planar(const uint8_t* coop, int64_t nb, int8_t* qs, uint32_t* ds, hipStream_t stream);
+hipError_t launch_coop_to_planar(const uint8_t* coop, int64_t nb, int8_t* qs, uint32_t* ds, uint32_t* hq,
+                                 hipStream_t stream);
 
 // Producers writing the planar Q8_1 workspace (row-major [M][K] inputs).
 // rms norm: h = X (+ R) (stored to H when non-null; H may equal X or R),
 // y = (h * 1/sqrt(mean(h^2) + eps)) * gamma; swiglu: y = silu(G) * U.
 hipError_t launch_rms_norm_q8_1(const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
-                                int64_t M, int8_t* qs, uint32_t* ds, hipStream_t stream);
+                                int64_t M, int8_t* qs, uint32_t* ds, uint32_t* hq, hipStream_t stream);
 hipError_t launch_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, int8_t* qs, uint32_t* ds,
-                              hipStream_t stream);
+                              uint32_t* hq, hipStream_t stream);
 
 hipError_t launch_fill_weights(uint8_t* W, int64_t n_blocks, uint64_t seed, int64_t first_block,
                                hipStream_t stream);

@@ -54,19 +54,22 @@ __device__ inline float exp_cody_waite(float x) {
 __device__ inline float silu(float g) { return g / (1.0f + exp_cody_waite(-g)); }
 
 // One 32-element block by the 8-lane group of lane L: values y at j, j+8,
-// j+16, j+24 (j = q8_lane_elem(L)) -> codes and ds in the planar workspace.
-__device__ inline void store_block8(const Q8Block8& b, int8_t* q, uint32_t* ds, int j) {
+// j+16, j+24 (j = q8_lane_elem(L)) -> codes, ds and the fp16 code pairs
+// (word p = elements p, p + 16) of the block in the planar workspace.
+__device__ inline void store_block8(const Q8Block8& b, int8_t* q, uint32_t* ds, uint32_t* hq, int j) {
     q[0] = (int8_t)b.q0;
     q[8] = (int8_t)b.q1;
     q[16] = (int8_t)b.q2;
     q[24] = (int8_t)b.q3;
+    hq[j] = codes_to_half2(b.q0, b.q2);
+    hq[j + 8] = codes_to_half2(b.q1, b.q3);
     if (j == 0) *ds = b.ds;
 }
 
 // y = silu(g) * u over M rows of K; 8 lanes per 32-element block.
 __global__ __launch_bounds__(256) void swiglu_q8_1_kernel(const float* __restrict__ G, const float* __restrict__ U,
                                                           int64_t n_blocks, int8_t* __restrict__ qs,
-                                                          uint32_t* __restrict__ ds) {
+                                                          uint32_t* __restrict__ ds, uint32_t* __restrict__ hq) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = t >> 3;
     if (blk >= n_blocks) return;  // whole 8-lane groups leave together
@@ -78,7 +81,7 @@ __global__ __launch_bounds__(256) void swiglu_q8_1_kernel(const float* __restric
         const float s = silu(G[e + 8 * i]);
         y[i] = s * U[e + 8 * i];
     }
-    store_block8(quantize_block8(y[0], y[1], y[2], y[3]), qs + e, ds + blk, j);
+    store_block8(quantize_block8(y[0], y[1], y[2], y[3]), qs + e, ds + blk, hq + blk * 16, j);
 }
 
 // One work-group of RMS_THREADS threads (16 waves) per row, with the
@@ -94,7 +97,8 @@ template <bool kLds, bool kRes, bool kGain>
 __global__ __launch_bounds__(RMS_THREADS) void rms_norm_q8_1_kernel(const float* X, const float* R, float* H,
                                                                     const float* __restrict__ gamma, float eps,
                                                                     int64_t K, int8_t* __restrict__ qs,
-                                                                    uint32_t* __restrict__ ds) {
+                                                                    uint32_t* __restrict__ ds,
+                                                                    uint32_t* __restrict__ hq) {
     extern __shared__ float sh[];  // kLds: h[K]
     __shared__ double part[RMS_WAVES];
     const int64_t m = blockIdx.x;
@@ -139,7 +143,8 @@ __global__ __launch_bounds__(RMS_THREADS) void rms_norm_q8_1_kernel(const float*
             if (!kLds && !h && kRes) v = v + r[e + 8 * i];
             y[i] = rms_y<kGain>(v, scale, kGain ? gcur[i] : 0.0f);
         }
-        store_block8(quantize_block8(y[0], y[1], y[2], y[3]), qs + m * K + e, ds + m * nb + b, j);
+        store_block8(quantize_block8(y[0], y[1], y[2], y[3]), qs + m * K + e, ds + m * nb + b,
+                     hq + (m * nb + b) * 16, j);
         if (kGain) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) gcur[i] = gnext[i];
@@ -149,33 +154,34 @@ __global__ __launch_bounds__(RMS_THREADS) void rms_norm_q8_1_kernel(const float*
 
 template <bool kLds>
 void launch_rms(bool res, bool gain, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const float* X,
-                const float* R, float* H, const float* gamma, float eps, int64_t K, int8_t* qs, uint32_t* ds) {
+                const float* R, float* H, const float* gamma, float eps, int64_t K, int8_t* qs, uint32_t* ds,
+                uint32_t* hq) {
     if (res && gain)
         hipLaunchKernelGGL((rms_norm_q8_1_kernel<kLds, true, true>), grid, block, lds, stream, X, R, H, gamma, eps, K,
-                           qs, ds);
+                           qs, ds, hq);
     else if (res)
         hipLaunchKernelGGL((rms_norm_q8_1_kernel<kLds, true, false>), grid, block, lds, stream, X, R, H, gamma, eps, K,
-                           qs, ds);
+                           qs, ds, hq);
     else if (gain)
         hipLaunchKernelGGL((rms_norm_q8_1_kernel<kLds, false, true>), grid, block, lds, stream, X, R, H, gamma, eps, K,
-                           qs, ds);
+                           qs, ds, hq);
     else
         hipLaunchKernelGGL((rms_norm_q8_1_kernel<kLds, false, false>), grid, block, lds, stream, X, R, H, gamma, eps,
-                           K, qs, ds);
+                           K, qs, ds, hq);
 }
 
 hipError_t launch_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, int8_t* qs, uint32_t* ds,
-                              hipStream_t stream) {
+                              uint32_t* hq, hipStream_t stream) {
     clear_launch_error();
     const int64_t n_blocks = (K / QK8_1) * M;
     const int64_t grid = (n_blocks * 8 + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(swiglu_q8_1_kernel, dim3((unsigned)grid), dim3(256), 0, stream, G, U, n_blocks, qs, ds);
+    hipLaunchKernelGGL(swiglu_q8_1_kernel, dim3((unsigned)grid), dim3(256), 0, stream, G, U, n_blocks, qs, ds, hq);
     return hipGetLastError();
 }
 
 hipError_t launch_rms_norm_q8_1(const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
-                                int64_t M, int8_t* qs, uint32_t* ds, hipStream_t stream) {
+                                int64_t M, int8_t* qs, uint32_t* ds, uint32_t* hq, hipStream_t stream) {
     clear_launch_error();
     if (M > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     const dim3 grid((unsigned)M), block(RMS_THREADS);
@@ -192,9 +198,9 @@ hipError_t launch_rms_norm_q8_1(const float* X, const float* R, float* H, const 
                 if (e != hipSuccess) return e;
             }
         }
-        launch_rms<true>(R != nullptr, gamma != nullptr, grid, block, lds, stream, X, R, H, gamma, eps, K, qs, ds);
+        launch_rms<true>(R != nullptr, gamma != nullptr, grid, block, lds, stream, X, R, H, gamma, eps, K, qs, ds, hq);
     } else {
-        launch_rms<false>(R != nullptr, gamma != nullptr, grid, block, 0, stream, X, R, H, gamma, eps, K, qs, ds);
+        launch_rms<false>(R != nullptr, gamma != nullptr, grid, block, 0, stream, X, R, H, gamma, eps, K, qs, ds, hq);
     }
     return hipGetLastError();
 }

@@ -52,6 +52,7 @@ __device__ inline void quantize_block_regs(const float (&x)[32], uint32_t (&q)[8
 template <int kLayout>
 __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restrict__ X, int64_t K, int64_t M,
                                                             int8_t* __restrict__ qs, uint32_t* __restrict__ ds,
+                                                            uint32_t* __restrict__ hq,
                                                             block_q8_1* __restrict__ blocks) {
     const int64_t nb = K / QK8_1;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -84,6 +85,18 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restr
         o[0] = v4i{(int)q[0], (int)q[1], (int)q[2], (int)q[3]};
         o[1] = v4i{(int)q[4], (int)q[5], (int)q[6], (int)q[7]};
         ds[m * nb + ib] = dsw;
+        // fp16 pairs: word p holds elements p and p + 16
+        v4i* h = reinterpret_cast<v4i*>(hq + (m * nb + ib) * 16);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            uint32_t pw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int p = 4 * w + i;
+                pw[i] = codes_to_half2((int8_t)(q[p >> 2] >> (8 * (p & 3))), (int8_t)(q[4 + (p >> 2)] >> (8 * (p & 3))));
+            }
+            h[w] = v4i{(int)pw[0], (int)pw[1], (int)pw[2], (int)pw[3]};
+        }
     }
     if (blocks != nullptr) {
         uint32_t* o = reinterpret_cast<uint32_t*>(blocks + m * nb + ib);
@@ -112,6 +125,7 @@ __global__ __launch_bounds__(256) void planar_to_blocks_kernel(const int8_t* __r
 // (quantize_block8); whole 8-lane groups are always active together.
 __global__ __launch_bounds__(256) void quantize_q8_1_rows_kernel(const float* __restrict__ X, int64_t K, int64_t M,
                                                                  int8_t* __restrict__ qs, uint32_t* __restrict__ ds,
+                                                                 uint32_t* __restrict__ hq,
                                                                  block_q8_1* __restrict__ blocks) {
     const int64_t nb = K / QK8_1;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -127,6 +141,8 @@ __global__ __launch_bounds__(256) void quantize_q8_1_rows_kernel(const float* __
         o[8] = (int8_t)b.q1;
         o[16] = (int8_t)b.q2;
         o[24] = (int8_t)b.q3;
+        hq[blk * 16 + j] = codes_to_half2(b.q0, b.q2);  // elements j, j + 16
+        hq[blk * 16 + j + 8] = codes_to_half2(b.q1, b.q3);  // elements j + 8, j + 24
         if (j == 0) ds[blk] = b.ds;
     }
     if (blocks != nullptr) {
@@ -139,7 +155,7 @@ __global__ __launch_bounds__(256) void quantize_q8_1_rows_kernel(const float* __
     }
 }
 
-hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds,
+hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds, uint32_t* hq,
                            block_q8_1* blocks, hipStream_t stream) {
     clear_launch_error();
     const int64_t total = (K / QK8_1) * M;
@@ -147,13 +163,13 @@ hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int
         const int64_t grid = (total * 8 + 255) / 256;
         if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
         hipLaunchKernelGGL(quantize_q8_1_rows_kernel, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs, ds,
-                           blocks);
+                           hq, blocks);
         return hipGetLastError();
     }
     const int64_t grid = (total + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(quantize_q8_1_kernel<LAYOUT_KM>, dim3((unsigned)grid), dim3(256), 0, stream, X, K, M, qs, ds,
-                       blocks);
+                       hq, blocks);
     return hipGetLastError();
 }
 

@@ -67,11 +67,14 @@ def test_can_handle_gates(L, pkg):
 
 
 def test_workspace_bytes(L):
+    """codes int8 [M][K], then ds uint32 [M][K/32], then the fp16 code pairs [M][K]
+    (2 bytes per code), each part at a 256-byte boundary."""
     K, M = 5120, 512
     qs = K * M
     ds_off = (qs + 255) // 256 * 256
-    assert L.iq4xs_workspace_bytes(K, M) == ds_off + M * (K // 32) * 4
-    assert L.iq4xs_workspace_bytes(256, 1) == 256 + 32
+    hq_off = (ds_off + M * (K // 32) * 4 + 255) // 256 * 256
+    assert L.iq4xs_workspace_bytes(K, M) == hq_off + 2 * K * M
+    assert L.iq4xs_workspace_bytes(256, 1) == 256 + 256 + 512
     assert L.iq4xs_workspace_bytes(0, 1) == 0 and L.iq4xs_workspace_bytes(100, 1) == 0
 
 

@@ -53,9 +53,9 @@ def test_noalloc_refuses_sizes_past_the_scratch(pkg, dev):
     L = pkg.lib()
     s = torch.cuda.current_stream().cuda_stream
     K, N = 17408, 64
-    limit = 64 << 20
-    M_over = 3500  # 17408 * 3500 * 1.125 bytes > 64 MiB
-    assert L.iq4xs_workspace_bytes(K, M_over) > limit >= L.iq4xs_workspace_bytes(K, 3400)
+    limit = 128 << 20
+    M_over = 2500  # 17408 * 2500 * 3.125 bytes > 128 MiB
+    assert L.iq4xs_workspace_bytes(K, M_over) > limit >= L.iq4xs_workspace_bytes(K, 2400)
     W = torch.zeros(N * K // 256 * 136, dtype=torch.uint8, device=dev)
     X = torch.zeros(16, device=dev)  # never read: the call is refused before any launch
     Y = torch.full((4,), 7.0, device=dev)
