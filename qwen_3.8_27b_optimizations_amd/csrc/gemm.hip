@@ -38,7 +38,8 @@
 //
 // Non-finite scales (an fp16 d of Inf/NaN) give NaN in the int8 kernels where
 // the reference's product would give +-Inf: the hi/lo split of an infinite
-// scale is Inf + NaN.  The fp16 kernel keeps the reference's +-Inf.
+// scale is Inf + NaN.  The fp16 kernel keeps the reference's +-Inf: no
+// infinite half of one scale meets a zero half of the other.
 //
 // MI355X mapping (64x64 int8 kernel).  A workgroup (4 waves) owns a 64-row x
 // 64-token output tile and walks K one 256-weight super-block at a time:
@@ -465,7 +466,8 @@ __global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const GemmGro
 //     read hit distinct bank groups.  Word p of a block pairs elements p and
 //     p + 16, which is exactly the k order of the weight fragment: lane half h
 //     of MFMA u takes qs bytes 8h + 4u .. + 3, low and high nibble of each.
-//   * Token scales: bf16 hi/lo pairs of d_x, [token][sub-block], per stage.
+//   * Token scales: bf16 hi/lo pairs of d_x, [token][sub-block], per stage,
+//     in two copies: lane half 1's has 0 for a non-finite d_x (see decode).
 // Each wave runs its 16 (sub-block, token block) steps of a super-block as a
 // software pipeline: step t issues its three MFMAs, each followed by the LDS
 // read that refills its A operand for step t + 1 and by a share of the VALU
@@ -483,10 +485,11 @@ constexpr int kVmcnt5 = 5 | (0x7 << 4) | (0xF << 8);
 
 constexpr int H_BN = 128, H_BM = 128, H_THREADS = 512;
 constexpr int H_ROW = 512;                           // LDS bytes per token row of a super-block
-constexpr int H_T_OFF = H_BM * H_ROW;                // token scale pairs, uint32 [128][8]
-constexpr int H_STAGE = H_T_OFF + H_BM * 8 * 4;      // 68 KB
+constexpr int H_T_OFF = H_BM * H_ROW;                // token scale pairs, uint32 [2][128][8]
+constexpr int H_T_COPY = H_BM * 8 * 4;               // copy h of them feeds lane half h
+constexpr int H_STAGE = H_T_OFF + 2 * H_T_COPY;      // 72 KB
 constexpr int H_LUT = 1024;                          // the code pair table
-// the table and two stages: 137 KB of gfx950's 160 KB of LDS per CU
+// the table and two stages: 145 KB of gfx950's 160 KB of LDS per CU
 
 __device__ inline int h_chunk(int m, int c) { return m * H_ROW + ((c ^ (m & 15)) << 4); }
 
@@ -582,11 +585,15 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
                                                LoadNext&& load_next) {
     // this wave's half of the 6-bit scales at sub-block positions 0-3
     const uint32_t h0 = (w.hdr.x & 0xFFFFu) | ((w.hdr.x >> (8 * kh)) & 0xFF0000u), h1 = w.hdr.y >> (16 * kh);
-    const float dw = half_bits_to_float(h0 & 0xFFFFu), dw_m32 = -32.0f * dw;
+    const float dw = half_bits_to_float(h0 & 0xFFFFu);
     // lane half h = 1 takes the low bf16 half of each weight scale; for an
-    // infinite or NaN d_w that half is 0 (the high half carries the Inf/NaN)
+    // infinite or NaN d_w that half is 0 and lane half 0 puts the high half
+    // in k slot 2i only, against d_x's high half (slot 2i + 1 meets d_x's low
+    // half, which may be 0): the scale tile is then +-Inf where the
+    // reference's d_w * d_x is, and NaN where it is
     const uint32_t hmask = h ? 0xFFFF0000u : 0u;
-    const bool zap = h && !__builtin_isfinite(dw);
+    const bool finite = __builtin_isfinite(dw), zap = h && !finite;
+    const uint32_t bsel = (h || finite) ? 0x07060706u : 0x0C0C0706u;
     // B operands of sub-block i, built in three parts spread over the steps
     // of the previous sub-block: the fp16 codes (b0: k 0-15, b1: k 16-31 of
     // the MFMA pair) and the scale column bsc: this row's d_w * (ls - 32)
@@ -594,13 +601,15 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
     // half in lane half 1, at k slots 2i, 2i + 1 of that half
     auto decode = [&](int i, int part, v4u& b0, v4u& b1, v4u& bsc) {
         if (part == 2) {
-            const uint32_t lsr = subblock_ls(h0, h1, i);  // ls + 32, 0..63
-            const float x = __builtin_fmaf(dw, (float)(int)lsr, dw_m32);  // exact: at most 16 significant bits
+            // d_w * (ls - 32), exact: at most 16 significant bits (as the
+            // product, not fma(d_w, ls, -32 d_w), which is Inf - Inf for an
+            // infinite d_w)
+            const float x = dw * (float)((int)subblock_ls(h0, h1, i) - 32);
             const uint32_t xb = __builtin_bit_cast(uint32_t, x);
             uint32_t v = __builtin_bit_cast(uint32_t, x - __builtin_bit_cast(float, xb & hmask));
             v = zap ? 0u : v;
             bsc = v4u{0u, 0u, 0u, 0u};
-            bsc[i] = __builtin_amdgcn_perm(v, v, 0x07060706u);
+            bsc[i] = __builtin_amdgcn_perm(v, v, bsel);
         } else {
             (part ? b1 : b0) = lut_pairs(lut, part ? w.qs[i].y : w.qs[i].x);
         }
@@ -614,7 +623,7 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
         if (r < 2)
             a = *reinterpret_cast<const v4u*>(st + h_chunk(m, 4 * s + 2 * h + r));
         else
-            a = *reinterpret_cast<const v4u*>(st + H_T_OFF + m * 32 + 16 * kh);
+            a = *reinterpret_cast<const v4u*>(st + H_T_OFF + h * H_T_COPY + m * 32 + 16 * kh);
     };
     // half q of the epilogue of step t: acc += sp * dp for accumulators 8q .. 8q + 7
     auto epilogue = [&](int t, const v16f& dp, const v16f& sp, int q) {
@@ -756,10 +765,15 @@ __global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp
     const uint32_t* dtile = ads + m0 * nb;
     const uint32_t doff = (uint32_t)(((m0 + tm < M) ? tm : M - 1 - m0) * nb + ts);
     auto load_d = [&](int64_t kb) { return *reinterpret_cast<const v2u*>(dtile + kb * 8 + doff); };
+    // copy 1 (lane half 1, which meets the weight scale's low half) has 0
+    // for a non-finite d_x, so that no Inf meets a zero low half (0 * Inf)
     auto store_d = [&](v2u d, uint8_t* stage) {
         uint32_t* t = reinterpret_cast<uint32_t*>(stage + H_T_OFF) + tm * 8 + ts;
-        *reinterpret_cast<v2u*>(t) = v2u{bf16_pair_f(half_bits_to_float(d.x & 0xFFFFu)),
-                                         bf16_pair_f(half_bits_to_float(d.y & 0xFFFFu))};
+        const float x0 = half_bits_to_float(d.x & 0xFFFFu), x1 = half_bits_to_float(d.y & 0xFFFFu);
+        const v2u p = v2u{bf16_pair_f(x0), bf16_pair_f(x1)};
+        *reinterpret_cast<v2u*>(t) = p;
+        *reinterpret_cast<v2u*>(t + H_T_COPY / 4) =
+            v2u{__builtin_isfinite(x0) ? p.x : 0u, __builtin_isfinite(x1) ? p.y : 0u};
     };
 
     v16f acc[4];

@@ -454,3 +454,60 @@ def test_deterministic_replay(pkg, dev):
     d = pkg.mul_mat(W, X[:K], K, N, 1)
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(c, d)
+
+
+# Non-finite fp16 super-block scales (+Inf, -Inf, NaN): every output keeps the reference's
+# class (finite within tolerance, +Inf, -Inf or NaN), as the reference's product
+# fp16(d_w) * fp16(d_x) * float(sumi * (ls - 32)) gives it.  An activation block whose Q8_1
+# scale overflows to +Inf (|x| >= 8.3e6) keeps it in the GEMV paths; the fp16 GEMM turns that
+# token's outputs into NaN instead (its scale MFMA meets the Inf with the zero k slots of the
+# other sub-blocks), so it is checked for the GEMV paths only.
+NONFINITE_D = np.array([0x7C00, 0xFC00, 0x7E00], np.uint16)
+
+
+def check_classes(y_ref, y_gpu, label):
+    ref_nan, gpu_nan = np.isnan(y_ref), np.isnan(y_gpu)
+    assert np.array_equal(ref_nan, gpu_nan), f"{label}: NaN positions differ"
+    for sgn in (1, -1):
+        assert np.array_equal(y_ref == sgn * np.inf, y_gpu == sgn * np.inf), f"{label}: {sgn:+d} Inf positions differ"
+    fin = np.isfinite(y_ref)
+    assert fin.any() and (~fin).any(), label
+    a, b = y_ref[fin].astype(np.float64), y_gpu[fin].astype(np.float64)
+    assert np.linalg.norm(a - b) <= REL_L2_TOL * np.linalg.norm(a), label
+
+
+def nonfinite_case(orc, M, inf_activation):
+    K, N = 2048, 2051
+    W = orc.gen_weights(K, N, seed=91)
+    blocks = W.reshape(-1, 136)
+    bpr = K // 256
+    for j, r in enumerate(range(0, N, 37)):  # one super-block of every 37th row gets a non-finite d
+        d = int(NONFINITE_D[j % 3])
+        blocks[r * bpr + (j % bpr), 0] = d & 0xFF
+        blocks[r * bpr + (j % bpr), 1] = d >> 8
+    X = orc.gen_activations(K * M, seed=92, outliers=True).reshape(M, K)
+    if inf_activation:
+        X[M // 2, 300:340] = 3.0e7  # activation blocks whose fp16 d_x overflows to +Inf
+    return K, N, W, X
+
+
+# M: bs=1 tile GEMV, matrix-core GEMV (4, 8), fp16 matrix-core GEMM (64 one tile, 200 two token tiles)
+@pytest.mark.parametrize("M", [1, 4, 8, 64, 200])
+def test_nonfinite_weight_scales_keep_reference_classes(pkg, orc, dev, M):
+    K, N, W, X = nonfinite_case(orc, M, inf_activation=False)
+    AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
+    ws = pkg.quantize_q8_1(D(X, dev), K, M, LAYOUT_MK)
+    Y = pkg.mul_mat_q8_1(D(W, dev), ws, K, N, M, LAYOUT_MK)
+    torch.cuda.synchronize()
+    y_ref = orc.gemm_semantics(W, AQ, K, N, M).T if M > 1 else orc.gemv_semantics(W, AQ, K, N)[None, :]
+    check_classes(y_ref, Y.cpu().numpy().reshape(M, N), f"non-finite weight scales, M={M}")
+
+
+@pytest.mark.parametrize("M", [4, 8])
+def test_infinite_activation_scale_in_gemv_paths(pkg, orc, dev, M):
+    K, N, W, X = nonfinite_case(orc, M, inf_activation=True)
+    AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
+    ws = pkg.quantize_q8_1(D(X, dev), K, M, LAYOUT_MK)
+    Y = pkg.mul_mat_q8_1(D(W, dev), ws, K, N, M, LAYOUT_MK, pkg.PATH_GEMV)
+    torch.cuda.synchronize()
+    check_classes(orc.gemm_semantics(W, AQ, K, N, M).T, Y.cpu().numpy().reshape(M, N), f"Inf d_x, M={M}")
