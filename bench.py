@@ -19,7 +19,7 @@ roofline  the GEMV kernel alone, on prequantised Q8_1 activations: a graph of
           algorithmic bytes / average launch duration.
 dequant   IQ4_XS -> fp32 (dequant_iq4xs_gpu) over the seven weight matrices.
 extra     bs = 2, 4, 8 (the same GEMV-only measurement with 1 % x20
-          outliers) and the int8-MFMA GEMM at M = 512 and 2048 (2*M*N*K over
+          outliers) and the matrix-core GEMM at M = 512 and 2048 (2*M*N*K over
           the average of back-to-back launches rotated over the layer copies).
 producers iq4xs_rms_norm_q8_1 (K=5120, with residual) and iq4xs_swiglu_q8_1
           (K=17408) at M = 1 and 512.
@@ -692,7 +692,7 @@ def main() -> int:
         "grouped_gemv": grouped,
         "small_batch_gemv": small,
         "gemm": {"peak_tops": INT8_PEAK_TOPS, "by_M": gemm,
-                 "kernel": "gemm_iq4xs_db_kernel (128x128) or gemm_iq4xs_mfma_kernel (64x64), chosen per shape"},
+                 "kernel": "gemm_f16_kernel: 128x128 tiles, exact integer products on v_mfma_f32_32x32x16_f16"},
         "dequant": dequant,
         "producers": producers,
         "model_stream": model,

@@ -51,9 +51,9 @@ extern "C" {
 #define IQ4XS_LAYOUT_MK 1 /* X[m*K + k], Y[m*N + n]  (ggml src1 / dst)                    */
 
 /* Kernel selection for iq4xs_mul_mat_q8_1 / iq4xs_subblock_sums */
-#define IQ4XS_PATH_AUTO -1 /* streaming GEMV for M <= 8, int8-MFMA GEMM above */
+#define IQ4XS_PATH_AUTO -1 /* streaming GEMV for M <= 8, matrix-core GEMM above */
 #define IQ4XS_PATH_GEMV 0  /* streaming GEMV (M <= 8 only)                   */
-#define IQ4XS_PATH_GEMM 1  /* int8-MFMA GEMM (any M)                         */
+#define IQ4XS_PATH_GEMM 1  /* matrix-core GEMM (any M)                       */
 
 /* ===================== standalone API (kernels/matmul_iq4xs) ===================== */
 
@@ -131,7 +131,7 @@ int gemm_iq4xs_lut_gpu(const void* W, const void* LUT, const float* X, float* Y,
 
 /* Replaces gemm_iq4xs_stock_dp4a_gpu, real_stock_dp4a_comparator.hip:505-548:
  * Y[n*M + m] = sum_k W[n,k] X[k*M + m].  M <= 8 runs the streaming GEMV,
- * larger M the int8-MFMA GEMM. */
+ * larger M the matrix-core GEMM. */
 int gemm_iq4xs_stock_dp4a_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
                               void* stream);
 

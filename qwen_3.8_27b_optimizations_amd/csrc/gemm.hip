@@ -55,7 +55,16 @@
 // LDS rows are 256 bytes; the 16-byte chunk index is XORed with (row & 15)
 // so the 32 lanes that read one k-chunk of 32 different rows hit 16
 // distinct chunk positions (no bank conflicts from the 256-byte row stride).
+#include <stdio.h>
 #include <stdlib.h>
+
+#include <algorithm>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <queue>
+#include <tuple>
+#include <vector>
 
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
@@ -578,7 +587,7 @@ struct HWeights {  // one super-block of this lane's weight row: header, and qs 
 // flight; the next sub-block's weights are decoded during the current one.
 // `w` is reloaded with the next super-block (load_next) once its last
 // sub-block is decoded, so one set of weight registers serves both.
-template <bool kDebug, typename LoadNext>
+template <bool kDebug, int T, typename LoadNext>
 __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t* lut, HWeights& w, v16f (&acc)[4],
                                                int kh, int h, int col, int lane, int64_t kb, int64_t m0, int64_t M,
                                                int64_t n, int64_t N, int64_t nb, int32_t* __restrict__ dbg,
@@ -614,12 +623,12 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
             (part ? b1 : b0) = lut_pairs(lut, part ? w.qs[i].y : w.qs[i].x);
         }
     };
-    // operand r of step t (token block j = t & 3, sub-block 4 kh + (t >> 2)):
+    // operand r of step t (token block j = t % T, sub-block 4 kh + t / T):
     // r = 0, 1: the A operands of the two code MFMAs; r = 2: the scale MFMA's
     // A operand, the bf16 pairs of d_x of this wave's 4 sub-blocks for token
     // 32 j + col
     auto frag = [&](int t, int r, v4u& a) {
-        const int m = 32 * (t & 3) + col, s = 4 * kh + (t >> 2);
+        const int m = 32 * (t % T) + col, s = 4 * kh + t / T;
         if (r < 2)
             a = *reinterpret_cast<const v4u*>(st + h_chunk(m, 4 * s + 2 * h + r));
         else
@@ -627,15 +636,15 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
     };
     // half q of the epilogue of step t: acc += sp * dp for accumulators 8q .. 8q + 7
     auto epilogue = [&](int t, const v16f& dp, const v16f& sp, int q) {
-        const int jp = t & 3;
+        const int jp = t % T;
 #pragma unroll
         for (int e = 8 * q; e < 8 * q + 8; ++e) {
             acc[jp][e] = __builtin_fmaf(sp[e], dp[e], acc[jp][e]);
             if (kDebug) {
-                const int s = 4 * kh + (t >> 2);
+                const int s = 4 * kh + t / T;
                 const int64_t mg = m0 + 32 * jp + mfma_c_row(e, lane);
                 if (mg < M && n < N)
-                    dbg[(mg * N + n) * nb + kb * 8 + s] = (int)dp[e] * (subblock_ls(h0, h1, t >> 2) - 32);
+                    dbg[(mg * N + n) * nb + kb * 8 + s] = (int)dp[e] * (subblock_ls(h0, h1, t / T) - 32);
             }
         }
         // pin the epilogue here: without it the optimiser sinks every FMA to
@@ -650,9 +659,10 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
     frag(0, 1, a1);
     frag(0, 2, ts);
     v16f dp, sp;
+    constexpr int STEPS = 4 * T;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        const int i = t >> 2, j = t & 3;
+    for (int t = 0; t < STEPS; ++t) {
+        const int i = t / T, j = t % T;
         // each MFMA is followed by the LDS read that refills its A operand for
         // step t + 1 and by a share of the VALU work (the FMAs of step t - 1,
         // then a part of the next sub-block's decode), so that the wave issues
@@ -661,77 +671,53 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
         v16f d = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a0), __builtin_bit_cast(v8h, b0),
                                                         v16f{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        if (t + 1 < 16) frag(t + 1, 0, a0);
+        if (t + 1 < STEPS) frag(t + 1, 0, a0);
         if (t > 0) epilogue(t - 1, dp, sp, 0);
         __builtin_amdgcn_sched_barrier(0);
         d = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a1), __builtin_bit_cast(v8h, b1), d, 0, 0,
                                                    0);
         __builtin_amdgcn_sched_barrier(0);
-        if (t + 1 < 16) frag(t + 1, 1, a1);
+        if (t + 1 < STEPS) frag(t + 1, 1, a1);
         if (t > 0) epilogue(t - 1, dp, sp, 1);
         __builtin_amdgcn_sched_barrier(0);
         const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ts),
                                                                 __builtin_bit_cast(v8bf, bsc), v16f{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        if (t + 1 < 16) frag(t + 1, 2, ts);
-        if (i < 3 && j < 3) decode(i + 1, j, nb0, nb1, nbsc);
-        if (i < 3 && j == 3) {
-            b0 = nb0;
-            b1 = nb1;
-            bsc = nbsc;
+        if (t + 1 < STEPS) frag(t + 1, 2, ts);
+        // the next sub-block's three decode parts: part p in step min(p, T - 1)
+        if (i < 3) {
+#pragma unroll
+            for (int part = 0; part < 3; ++part)
+                if (j == (part < T ? part : T - 1)) decode(i + 1, part, nb0, nb1, nbsc);
+            if (j == T - 1) {
+                b0 = nb0;
+                b1 = nb1;
+                bsc = nbsc;
+            }
         }
-        if (t == 10) load_next(w);  // decode(3) in steps 8-10 was the last use of w
+        if (i == 2 && j == T - 1) load_next(w);  // decode(3) above was the last use of w
         dp = d;
         sp = sc;
         __builtin_amdgcn_sched_barrier(0);
     }
-    epilogue(15, dp, sp, 0);
-    epilogue(15, dp, sp, 1);
+    epilogue(STEPS - 1, dp, sp, 0);
+    epilogue(STEPS - 1, dp, sp, 1);
 }
 
-template <bool kDebug, bool kGroup>
-__global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp, const uint32_t* __restrict__ ahq,
-                                                             const uint32_t* __restrict__ ads, int64_t K, int64_t M,
-                                                             int64_t ldy_n, int tiles_x, int tiles,
-                                                             int32_t* __restrict__ dbg) {
-    // LDS: the 1 KB code pair table at address 0, then the two stages
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[H_LUT + 2 * H_STAGE];
+// One 128-row x 32T-token tile (T token blocks per wave; the per-output
+// arithmetic does not depend on T, so neither do the results).
+// W, Y, N, ldy_m: the tile's matrix, whose first row tile is tile0.
+template <bool kDebug, int T>
+__device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* __restrict__ Y, int64_t N,
+                                         int64_t ldy_m, int tile0, const uint32_t* __restrict__ ahq,
+                                         const uint32_t* __restrict__ ads, int64_t K, int64_t M, int64_t ldy_n, int bx,
+                                         int by, uint8_t* smem, int32_t* __restrict__ dbg) {
     uint8_t(*const stages)[H_STAGE] = reinterpret_cast<uint8_t(*)[H_STAGE]>(smem + H_LUT);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
     const int rg = wave & 3, kh = wave >> 2, h = lane >> 5, col = lane & 31;
-
-    // XCD-aware tile order: the 8 XCDs take workgroups round-robin, so
-    // workgroup b runs on XCD b % 8; each XCD is given a contiguous range of
-    // the token-major tile order, so its tiles share few token tiles (L2).
-    int tile;
-    {
-        const int b = (int)blockIdx.x, x = b & 7, q = tiles >> 3, r = tiles & 7;
-        tile = x * q + min(x, r) + (b >> 3);
-    }
-    const int bx = tile % tiles_x, by = tile / tiles_x;
-    // the matrix of this tile: gemm_select's choice, by the logical tile index
-    const uint8_t* W = grp.W[0];
-    float* Y = grp.Y[0];
-    int64_t N = grp.N[0], ldy_m = grp.ldy_m[0];
-    int tile0 = 0;
-    if (kGroup) {
-        int gsel = 0;
-#pragma unroll
-        for (int i = 0; i + 1 < GEMV_GROUP_MAX; ++i) gsel += bx >= grp.tile_end[i] ? 1 : 0;
-#pragma unroll
-        for (int i = 1; i < GEMV_GROUP_MAX; ++i) {
-            if (gsel == i) {
-                W = grp.W[i];
-                Y = grp.Y[i];
-                N = grp.N[i];
-                ldy_m = grp.ldy_m[i];
-                tile0 = grp.tile_end[i - 1];
-            }
-        }
-    }
     const int64_t n0 = (int64_t)(bx - tile0) * H_BN;
-    const int64_t m0 = (int64_t)by * H_BM;
+    const int64_t m0 = (int64_t)by * (32 * T);
     const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
 
     // ---- this lane's weight row (rows past N repeat the last; never stored)
@@ -745,19 +731,23 @@ __global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp
         for (int i = 0; i < 4; ++i) g.qs[i] = *reinterpret_cast<const v2u*>(p + 8 + 16 * (4 * kh + i) + 8 * h);
     };
 
-    // ---- token staging: instruction i of this wave fills LDS chunks
-    // (wave * 8 + i) * 64 + lane of a stage (token row chunk >> 5, chunk & 31)
-    // (16 * wave + 2 * i + h, chunk col ^ (2 i + h) of that row: the swizzle)
+    // ---- token staging (32 T token rows of 512 bytes): instruction i of this
+    // wave fills LDS chunks (wave * 2T + i) * 64 + lane of a stage, i.e. row
+    // 4T wave + 2i + h, chunk col ^ (row & 15) of it (the swizzle)
     const uint8_t* xtile = reinterpret_cast<const uint8_t*>(ahq) + m0 * (2 * K);
-    const int xrow = 16 * wave + h, xlast = (int)min<int64_t>(M - 1 - m0, H_BM - 1);  // rows past M repeat the last
-    const uint32_t xstride = (uint32_t)(2 * K), xcol = 16u * (uint32_t)(col ^ h);
-    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_addr(&stages[0][0]) + wave * 8 * 1024);
+    const int xrow = 4 * T * wave + h, xlast = (int)min<int64_t>(M - 1 - m0, 32 * T - 1);  // rows past M repeat the last
+    const uint32_t xstride = (uint32_t)(2 * K);
+    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_addr(&stages[0][0]) + wave * 2 * T * 1024);
+    // for T != 3 the bits of xrow & 15 and of 2i are disjoint, so the
+    // swizzled chunk is (col ^ (xrow & 15)) ^ 2i: one XOR per copy
+    const uint32_t xcol = 16u * (uint32_t)(col ^ (xrow & 15));
     auto issue_x = [&](int64_t kb, int stage) {
         const uint8_t* src = xtile + kb * 512;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t voff = (uint32_t)min(xrow + 2 * i, xlast) * xstride + (xcol ^ (32u * i));
-            dma16(src, voff, lds_wave + stage * H_STAGE + i * 1024);
+        for (int i = 0; i < 2 * T; ++i) {
+            const int m = xrow + 2 * i;
+            const uint32_t c16 = T == 3 ? 16u * (uint32_t)(col ^ (m & 15)) : (xcol ^ (32u * i));
+            dma16(src, (uint32_t)min(m, xlast) * xstride + c16, lds_wave + stage * H_STAGE + i * 1024);
         }
     };
     // token scales: thread tid -> token tid >> 2, sub-blocks 2 (tid & 3), + 1
@@ -799,15 +789,15 @@ __global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp
     // the other; wc holds kb's weights, wo kb + 1's
     // The loads are issued unconditionally (past the end they repeat the last
     // super-block into registers and a stage that nothing reads any more), so
-    // that every iteration issues the same sequence: 8 copies + 1 token-scale
-    // load at the start, 5 weight loads at step 10; the wait before the
+    // that every iteration issues the same sequence: 2T copies + 1 token-scale
+    // load at the start, 5 weight loads after sub-block 2; the wait before the
     // barrier then leaves exactly the 5 weight loads in flight.
     auto superblock = [&](int64_t kb, HWeights& wc) {
         const int cur = (int)(kb & 1);
         const int64_t kb1 = min(kb + 1, bpr - 1), kb2 = min(kb + 2, bpr - 1);
         issue_x(kb1, cur ^ 1);
         v2u dnext = load_d(kb1);
-        f16_superblock<kDebug>(stages[cur], smem, wc, acc, kh, h, col, lane, kb, m0, M, n, N, nb, dbg,
+        f16_superblock<kDebug, T>(stages[cur], smem, wc, acc, kh, h, col, lane, kb, m0, M, n, N, nb, dbg,
                                [&](HWeights& g) { load_w(g, kb2); });
         // this thread's direct-to-LDS copies and token scales have landed; the
         // 5 weight loads of super-block kb + 2, issued after them, may still
@@ -833,18 +823,13 @@ __global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp
     }
     if (kb < bpr) superblock(kb, w);
 
-    // the two sub-block halves of each row group add their partial sums: kh = 1
-    // hands blocks 0, 1 to kh = 0 and takes blocks 2, 3 (constant indices only:
-    // a runtime index into acc would put it in scratch memory)
+    // the two sub-block halves of each row group add their partial sums:
+    // kh = 0 finalises token blocks j < (T + 1) / 2, kh = 1 the others, each
+    // taking the other half's partial sums through LDS (constant indices
+    // only: a runtime index into acc would put it in scratch memory)
+    constexpr int HALF = (T + 1) / 2;
     float* red = reinterpret_cast<float*>(&stages[0][0]);  // both stages are free now
-    auto put = [&](const v16f& a, int slot) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) red[((rg * 2 + kh) * 2 + slot) * 1024 + e * 64 + lane] = a[e];
-    };
-    auto take = [&](v16f& a, int slot) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) a[e] += red[((rg * 2 + (kh ^ 1)) * 2 + slot) * 1024 + e * 64 + lane];
-    };
+    auto slot = [&](int from_kh, int j) { return red + ((rg * 2 + from_kh) * 4 + j) * 1024 + lane; };
     auto store = [&](const v16f& a, int j) {
         if (n >= N) return;
 #pragma unroll
@@ -853,24 +838,94 @@ __global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp
             if (mg < M) Y[mg * ldy_m + n * ldy_n] = a[e];
         }
     };
-    if (kh) {
-        put(acc[0], 0);
-        put(acc[1], 1);
-    } else {
-        put(acc[2], 0);
-        put(acc[3], 1);
+#pragma unroll
+    for (int j = 0; j < T; ++j) {
+        if ((j < HALF) == (kh == 1)) {  // the other half finalises block j
+#pragma unroll
+            for (int e = 0; e < 16; ++e) slot(kh, j)[e * 64] = acc[j][e];
+        }
     }
     __syncthreads();
-    if (kh) {
-        take(acc[2], 0);
-        take(acc[3], 1);
-        store(acc[2], 2);
-        store(acc[3], 3);
-    } else {
-        take(acc[0], 0);
-        take(acc[1], 1);
-        store(acc[0], 0);
-        store(acc[1], 1);
+#pragma unroll
+    for (int j = 0; j < T; ++j) {
+        if ((j < HALF) == (kh == 0)) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][e] += slot(kh ^ 1, j)[e * 64];
+            store(acc[j], j);
+        }
+    }
+}
+
+// Workgroups of a launch fall into up to F16_SEGS segments, each a range of
+// row tiles (128 rows) x all tokens in tiles of 32T tokens; segment 0's
+// workgroups take their tiles in XCD-aware order.  A host-side plan picks
+// the segments so that the workgroups fill the CUs' rounds evenly.
+constexpr int F16_SEGS = 3;
+struct F16Seg {
+    int wg_end;  // one past this segment's last workgroup
+    int rt0;     // first row tile
+    int rts;     // row tiles
+    int T;       // token blocks (of 32) per tile: 1..4
+};
+struct F16Plan {
+    F16Seg seg[F16_SEGS];
+};
+
+template <bool kDebug, bool kGroup>
+__global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp, const uint32_t* __restrict__ ahq,
+                                                             const uint32_t* __restrict__ ads, int64_t K, int64_t M,
+                                                             int64_t ldy_n, const F16Plan plan,
+                                                             int32_t* __restrict__ dbg) {
+    // LDS: the 1 KB code pair table at address 0, then the two stages
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[H_LUT + 2 * H_STAGE];
+    const int b = (int)blockIdx.x;
+    // the segment (scalar selects on the by-value plan)
+    int g = 0;
+#pragma unroll
+    for (int i = 0; i + 1 < F16_SEGS; ++i) g += b >= plan.seg[i].wg_end ? 1 : 0;
+    F16Seg sg = plan.seg[0];
+    int start = 0;
+#pragma unroll
+    for (int i = 1; i < F16_SEGS; ++i) {
+        if (g == i) {
+            sg = plan.seg[i];
+            start = plan.seg[i - 1].wg_end;
+        }
+    }
+    int tile = b - start;
+    if (g == 0) {
+        // XCD-aware tile order: the 8 XCDs take workgroups round-robin, so
+        // workgroup b runs on XCD b % 8; each XCD is given a contiguous range
+        // of the token-major tile order, so its tiles share few token tiles
+        const int tiles = sg.wg_end, x = b & 7, q = tiles >> 3, r = tiles & 7;
+        tile = x * q + min(x, r) + (b >> 3);
+    }
+    const int bx = sg.rt0 + tile % sg.rts, by = tile / sg.rts;
+    // the matrix of this tile: gemm_select's choice, by the logical tile index
+    const uint8_t* W = grp.W[0];
+    float* Y = grp.Y[0];
+    int64_t N = grp.N[0], ldy_m = grp.ldy_m[0];
+    int tile0 = 0;
+    if (kGroup) {
+        int gsel = 0;
+#pragma unroll
+        for (int i = 0; i + 1 < GEMV_GROUP_MAX; ++i) gsel += bx >= grp.tile_end[i] ? 1 : 0;
+#pragma unroll
+        for (int i = 1; i < GEMV_GROUP_MAX; ++i) {
+            if (gsel == i) {
+                W = grp.W[i];
+                Y = grp.Y[i];
+                N = grp.N[i];
+                ldy_m = grp.ldy_m[i];
+                tile0 = grp.tile_end[i - 1];
+            }
+        }
+    }
+    switch (sg.T) {
+        case 1: f16_tile<kDebug, 1>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+        case 2: f16_tile<kDebug, 2>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+        case 3: f16_tile<kDebug, 3>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+        default: f16_tile<kDebug, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
     }
 }
 
@@ -882,14 +937,124 @@ static int gemm_kind() {
     return kind;
 }
 
+// Time of one workgroup of T token blocks relative to T = 4 with every CU
+// busy, for the round planner below (per-tile work is T token blocks against
+// the same weight decode, DMA and barrier cost per super-block).  Measured
+// on q_proj (K = 5120) at M = 512 with every workgroup of one size: 1, 2, 3
+// or 4 token blocks in 35.9, 47.4, 57.7, 77.3 us per round.
+static double f16_tile_cost(int T) {
+    static const double c[5] = {0.0, 0.46, 0.61, 0.75, 1.0};
+    return c[T < 1 ? 1 : (T > 4 ? 4 : T)];
+}
+
+// A launch of fewer workgroups than CUs runs each of them faster (less
+// contention for L2 and HBM): o_proj at M = 512, 160 workgroups of 4 token
+// blocks, takes 0.85x the per-super-block time of 256.  Modelled as
+// alpha + (1 - alpha) * busy fraction.
+static double f16_occupancy(int64_t wgs, int cus) {
+    const double alpha = 0.6, f = wgs >= cus ? 1.0 : (double)wgs / cus;
+    return alpha + (1.0 - alpha) * f;
+}
+
+static int64_t f16_token_tiles(int64_t M, int T) { return (M + 32 * T - 1) / (32 * T); }
+
+// Makespan of the plan's workgroups, dispatched in order to `cus` CUs that
+// each run one at a time (one workgroup fills a CU's LDS).
+static double f16_makespan(const F16Plan& p, int cus) {
+    std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
+    for (int c = 0; c < cus; ++c) free_at.push(0.0);
+    const double occ = f16_occupancy(p.seg[F16_SEGS - 1].wg_end, cus);
+    double end = 0.0;
+    int start = 0;
+    for (int g = 0; g < F16_SEGS; ++g) {
+        const double d = f16_tile_cost(p.seg[g].T) * occ;
+        for (int w = start; w < p.seg[g].wg_end; ++w) {
+            const double t = free_at.top() + d;
+            free_at.pop();
+            free_at.push(t);
+            end = std::max(end, t);
+        }
+        start = p.seg[g].wg_end;
+    }
+    return end;
+}
+
+static F16Plan f16_plan_of(std::initializer_list<std::pair<int64_t, int>> segs, int64_t M) {
+    F16Plan p{};
+    int64_t rt = 0, wg = 0;
+    int g = 0;
+    for (const auto& sgm : segs) {
+        p.seg[g] = F16Seg{0, (int)rt, (int)sgm.first, sgm.second};
+        wg += sgm.first * f16_token_tiles(M, sgm.second);
+        p.seg[g].wg_end = (int)wg;
+        rt += sgm.first;
+        ++g;
+    }
+    for (; g < F16_SEGS; ++g) p.seg[g] = F16Seg{(int)wg, (int)rt, 1, 4};  // empty
+    return p;
+}
+
+// The tiling of `row_tiles` row tiles x M tokens: one segment of one token
+// tile size, or a bulk of whole rounds plus a tail of smaller tiles that
+// spreads the last round over the CUs -- whichever finishes first by
+// f16_makespan.  A shape's plan depends on the shape and the CU count only,
+// and no plan changes a result bit.
+static F16Plan f16_plan(int64_t row_tiles, int64_t M) {
+    static const int forced = []() {
+        const char* v = getenv("IQ4XS_GEMM_T");  // tuning override: one segment of this token tile size
+        const int t = v ? atoi(v) : 0;
+        return (t >= 1 && t <= 4) ? t : 0;
+    }();
+    if (forced) return f16_plan_of({{row_tiles, forced}}, M);
+    const int cus = device_cu_count();
+    static std::mutex mu;
+    static std::map<std::tuple<int64_t, int64_t, int>, F16Plan> cache;
+    const auto key = std::make_tuple(row_tiles, M, cus);
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        const auto it = cache.find(key);
+        if (it != cache.end()) return it->second;
+    }
+    F16Plan best = f16_plan_of({{row_tiles, 4}}, M);
+    double best_t = f16_makespan(best, cus);
+    auto consider = [&](const F16Plan& p) {
+        const double t = f16_makespan(p, cus);
+        if (t < best_t - 1e-9) {
+            best = p;
+            best_t = t;
+        }
+    };
+    for (int T = 3; T >= 1; --T) consider(f16_plan_of({{row_tiles, T}}, M));
+    for (int Tb = 4; Tb >= 2; --Tb) {
+        const int64_t per_rt = f16_token_tiles(M, Tb);
+        const int64_t rounds = row_tiles * per_rt / cus;
+        for (int64_t k = rounds; k >= 1 && k + 2 >= rounds; --k) {
+            const int64_t rb = k * cus / per_rt;  // whole row tiles within k rounds
+            if (rb <= 0 || rb >= row_tiles) continue;
+            for (int Tt = Tb - 1; Tt >= 1; --Tt) consider(f16_plan_of({{rb, Tb}, {row_tiles - rb, Tt}}, M));
+        }
+    }
+    if (getenv("IQ4XS_GEMM_PLAN_LOG") != nullptr) {  // tuning aid: the chosen segments, on stderr
+        fprintf(stderr, "[iq4xs] gemm plan row_tiles=%lld M=%lld:", (long long)row_tiles, (long long)M);
+        for (int g = 0; g < F16_SEGS; ++g)
+            fprintf(stderr, " [wg_end=%d rt0=%d rts=%d T=%d]", best.seg[g].wg_end, best.seg[g].rt0, best.seg[g].rts,
+                    best.seg[g].T);
+        fprintf(stderr, " est=%.3f\n", best_t);
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    cache.emplace(key, best);
+    return best;
+}
+
 template <bool kDebug, bool kGroup>
-static hipError_t launch_f16_kernel(const GemmGroup& grp, int64_t tiles_x, const uint32_t* ahq, const uint32_t* ads,
+static hipError_t launch_f16_kernel(const GemmGroup& grp, int64_t row_tiles, const uint32_t* ahq, const uint32_t* ads,
                                     int64_t K, int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
-    const int64_t tiles_y = (M + H_BM - 1) / H_BM;
-    const int64_t tiles = tiles_x * tiles_y;
-    if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((gemm_f16_kernel<kDebug, kGroup>), dim3((unsigned)tiles), dim3(H_THREADS), 0, stream, grp, ahq,
-                       ads, K, M, ldy_n, (int)tiles_x, (int)tiles, dbg);
+    if (row_tiles * f16_token_tiles(M, 1) > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    const F16Plan plan = kDebug ? f16_plan_of({{row_tiles, 4}}, M) : f16_plan(row_tiles, M);
+    const int wgs = plan.seg[F16_SEGS - 1].wg_end;
+    if (wgs <= 0) return hipSuccess;
+    hipLaunchKernelGGL((gemm_f16_kernel<kDebug, kGroup>), dim3((unsigned)wgs), dim3(H_THREADS), 0, stream, grp, ahq,
+                       ads, K, M, ldy_n, plan, dbg);
     return hipGetLastError();
 }
 

@@ -71,7 +71,7 @@ hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads,
                        int64_t K, int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
                        hipStream_t stream);
 
-// Y[i] = W[i] x for i < count <= GEMV_GROUP_MAX on the int8 MFMA path, one
+// Y[i] = W[i] x for i < count <= GEMV_GROUP_MAX on the matrix-core GEMM path, one
 // launch; Y[i] is [M][N[i]] (layout_mk) or [N[i]][M].
 hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N, const int8_t* aqs,
                              const uint32_t* ads, const uint32_t* ahq, int64_t K, int64_t M, bool layout_mk,
