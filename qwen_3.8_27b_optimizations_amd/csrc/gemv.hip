@@ -661,6 +661,21 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     if (split) fused_load(fx, X, sk, tasks, tid, nthreads);
     RmsBatch rb;  // the RMS prologue's pass-1 loads (one batch: K <= RMS_ONE_BATCH_K), also ahead of the prefetch
     if (kRmsOn) rms_load<kRmsRes>(rb, X, rms.R, 4 * tid, K);
+    // and every gain the quantisation pass will read (its blocks b0 + STEP*i,
+    // clamped), so that pass waits for neither the weight prefetch (vmcnt
+    // retires in order) nor a round trip of its own
+    constexpr int RMS_STEP = RMS_THREADS / 8;
+    constexpr int RMS_Q_ROUNDS = (int)((RMS_ONE_BATCH_K / QK8_1 + RMS_STEP - 1) / RMS_STEP);
+    float gain[RMS_Q_ROUNDS][4];
+    if constexpr (kRmsOn && kRmsGain) {
+        const int j = q8_lane_elem(tid & 7);
+#pragma unroll
+        for (int r = 0; r < RMS_Q_ROUNDS; ++r) {
+            const int b = min((tid >> 3) + RMS_STEP * r, nb - 1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gain[r][i] = rms.gamma[b * QK8_1 + j + 8 * i];
+        }
+    }
     // Every weight load is unconditional (steps past this wave's last one
     // repeat it), so the wait counts are compile-time exact.
     StepRegs buf[D];
@@ -682,34 +697,22 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
         float* shh = reinterpret_cast<float*>(lds + h_off);
         const double acc = rms_accumulate<kRmsRes, true>(rb, blockIdx.x == 0 ? rms.H : nullptr, shh, 4 * tid, K, 0.0);
         const int j = q8_lane_elem(tid & 7);
-        constexpr int STEP = RMS_THREADS / 8;
-        const int b0 = tid >> 3;
-        float gcur[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (kRmsGain) {
-            const int e = (b0 < nb ? b0 : nb - 1) * QK8_1 + j;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) gcur[i] = rms.gamma[e + 8 * i];
-        }
         const float scale = rms_scale(rms_reduce(acc, rms_part, tid), K, rms.eps);
-        for (int b = b0; b < nb; b += STEP) {  // uniform per 8-lane group
-            const int e = b * QK8_1 + j;
-            float gnext[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (kRmsGain) {
-                const int bn = b + STEP < nb ? b + STEP : nb - 1;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) gnext[i] = rms.gamma[bn * QK8_1 + j + 8 * i];
+        for (int r = 0; r < RMS_Q_ROUNDS; ++r) {
+            const int b = (tid >> 3) + RMS_STEP * r;
+            if (b < nb) {  // uniform per 8-lane group
+                const int e = b * QK8_1 + j;
+                float y[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[i] = rms_y<kRmsGain>(shh[e + 8 * i], scale, kRmsGain ? gain[r][i] : 0.0f);
+                const Q8Block8 q = quantize_block8(y[0], y[1], y[2], y[3]);
+                sq[e] = (int8_t)q.q0;
+                sq[e + 8] = (int8_t)q.q1;
+                sq[e + 16] = (int8_t)q.q2;
+                sq[e + 24] = (int8_t)q.q3;
+                if (j == 0) sdx[b] = half_bits_to_float(q.ds & 0xFFFFu);
             }
-            float y[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) y[i] = rms_y<kRmsGain>(shh[e + 8 * i], scale, gcur[i]);
-            const Q8Block8 q = quantize_block8(y[0], y[1], y[2], y[3]);
-            sq[e] = (int8_t)q.q0;
-            sq[e + 8] = (int8_t)q.q1;
-            sq[e + 16] = (int8_t)q.q2;
-            sq[e + 24] = (int8_t)q.q3;
-            if (j == 0) sdx[b] = half_bits_to_float(q.ds & 0xFFFFu);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) gcur[i] = gnext[i];
         }
     } else if (split) {
         fused_store(fx, sq, sdx, tasks, tid, nthreads);
@@ -874,6 +877,23 @@ static int64_t tile_rows(int64_t bpr, int64_t N) {
     return ((units + tiles - 1) / tiles) * g;
 }
 
+// Rows per tile of a grouped launch: tile_rows of the summed rows, raised (by
+// whole steps) until the per-matrix tiles, each rounded up, fit the same
+// number of tiles -- otherwise three matrices round up to a tile past one per CU.
+static int64_t group_tile_rows(int64_t bpr, const int64_t* Ns, int count) {
+    const int64_t g = 8 / std::gcd<int64_t, int64_t>(bpr, 8);
+    int64_t rows = 0;
+    for (int i = 0; i < count; ++i) rows += Ns[i];
+    int64_t R = tile_rows(bpr, rows);
+    const int64_t cap = std::max<int64_t>((rows + R - 1) / R, count);  // reached once R >= every N
+    for (;;) {
+        int64_t t = 0;
+        for (int i = 0; i < count; ++i) t += (Ns[i] + R - 1) / R;
+        if (t <= cap) return R;
+        R += g;
+    }
+}
+
 // One launch over the matrices of `mats` (count >= 1, all with K columns);
 // hipErrorNotSupported when a tile's LDS does not fit.
 struct TileMat {
@@ -922,9 +942,12 @@ static hipError_t launch_tile_group(const TileMat* mats, int count, const int8_t
                                     const float* X, int64_t sc, int64_t sk, int64_t K, int64_t ldy_n, int32_t* dbg,
                                     hipStream_t stream) {
     const int64_t bpr = K / QK_K;
-    int64_t rows = 0;
-    for (int i = 0; i < count; ++i) rows += mats[i].N;
-    const int64_t R = tile_rows(bpr, rows);
+    int64_t rows = 0, Ns[GEMV_GROUP_MAX];
+    for (int i = 0; i < count; ++i) {
+        rows += mats[i].N;
+        Ns[i] = mats[i].N;
+    }
+    const int64_t R = group_tile_rows(bpr, Ns, count);
     if (R * bpr * BLOCK_BYTES >= ((int64_t)1 << 31) || rows >= ((int64_t)1 << 30)) return hipErrorNotSupported;
     static const int depth = tuning_knob("IQ4XS_GEMV_TILE_D", 2, 2, 4);
     if (depth == 3) return launch_tile_d<C, 3>(mats, count, aqs, ads, X, sc, sk, K, ldy_n, dbg, R, stream);
@@ -1070,7 +1093,7 @@ hipError_t launch_gemv_rms_group(int count, const uint8_t* const* W, float* cons
     if (count < 1 || count > GEMV_GROUP_MAX || bpr < 8 || K > RMS_ONE_BATCH_K) return hipErrorNotSupported;
     int64_t rows = 0;
     for (int i = 0; i < count; ++i) rows += N[i];
-    const int64_t Rr = tile_rows(bpr, rows);
+    const int64_t Rr = group_tile_rows(bpr, N, count);
     if (Rr * bpr * BLOCK_BYTES >= ((int64_t)1 << 31) || rows >= ((int64_t)1 << 30)) return hipErrorNotSupported;
     GemvGroup grp{};
     int64_t wgs = 0;

@@ -62,13 +62,36 @@ __device__ inline double rms_accumulate(RmsBatch& b, float* h, float* sh, int64_
     return acc;
 }
 
+// A double moved across lanes by one DPP control (both halves).
+template <int kCtrl>
+__device__ inline double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, kCtrl, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), kCtrl, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
 // The work-group's sum of squares from every thread's acc (part: RMS_WAVES
 // doubles of LDS).  Contains the __syncthreads that also orders pass 1's
 // stores before pass 2's reads.
+//
+// The wave sum is the xor butterfly acc += acc[lane ^ o], o = 32, 16, ..., 1.
+// o = 32 and 16 cross DPP rows and go through ds_bpermute; the other four
+// steps are DPP moves: row_ror:8 is lane ^ 8 within a row; row_ror:4 reads
+// lane (i + 4) mod 16, which differs from i ^ 4 by 8, and after the o = 8
+// step every lane holds the same value as its lane ^ 8 (a + b = b + a
+// exactly), so it reads the value lane ^ 4 holds; quad_perm [2,3,0,1] and
+// [1,0,3,2] are lane ^ 2 and lane ^ 1.  Every lane therefore adds the same
+// two doubles as the shuffle butterfly: the same bits, without four of its
+// six LDS round trips.
 __device__ inline double rms_reduce(double acc, double* part, int t) {
 #pragma clang fp contract(off)
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc = acc + __shfl_xor(acc, o, 64);
+    acc = acc + __shfl_xor(acc, 32, 64);
+    acc = acc + __shfl_xor(acc, 16, 64);
+    acc = acc + dpp_f64<0x128>(acc);  // row_ror:8
+    acc = acc + dpp_f64<0x124>(acc);  // row_ror:4
+    acc = acc + dpp_f64<0x4E>(acc);   // quad_perm [2,3,0,1]
+    acc = acc + dpp_f64<0xB1>(acc);   // quad_perm [1,0,3,2]
     if ((t & 63) == 0) part[t >> 6] = acc;
     __syncthreads();
     double p[RMS_WAVES];
