@@ -214,7 +214,7 @@ int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void
  * projection as separate ggml ops.
  *   - H (may be NULL) must not overlap X or R, and no Y[i] may overlap X, R or H
  *     (in-place forms are rejected with hipErrorInvalidValue);
- *   - X, R, H 16-byte aligned; K % 256 == 0, eps >= 0;
+ *   - X, R, H, gamma 16-byte aligned; K % 256 == 0, eps >= 0;
  *   - hipErrorNotSupported for K < 2048 or K > 8192, or when the row does not
  *     fit the kernel's LDS: use the two calls. */
 int iq4xs_rms_norm_mul_mat_group(int count, const void* const* W, float* const* Y, const int64_t* N, const float* X,

@@ -410,7 +410,8 @@ int iq4xs_rms_norm_mul_mat_group(int count, const void* const* W, float* const* 
                                  const float* R, float* H, const float* gamma, float eps, int64_t K, void* stream) {
     if (count < 1 || count > GEMV_GROUP_MAX || !W || !Y || !N || !X || !valid_k(K) || K >= MAX_DIM)
         return hipErrorInvalidValue;
-    if (!(eps >= 0.0f) || !aligned16(X) || !aligned16(R) || !aligned16(H)) return hipErrorInvalidValue;
+    if (!(eps >= 0.0f) || !aligned16(X) || !aligned16(R) || !aligned16(H) || !aligned16(gamma))
+        return hipErrorInvalidValue;
     // workgroup 0 writes H while the others still read X and R: no aliasing
     const size_t bytes = (size_t)K * sizeof(float);
     if (overlaps(H, bytes, X, bytes) || overlaps(H, bytes, R, bytes)) return hipErrorInvalidValue;

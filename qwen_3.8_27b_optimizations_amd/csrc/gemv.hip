@@ -661,20 +661,16 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     if (split) fused_load(fx, X, sk, tasks, tid, nthreads);
     RmsBatch rb;  // the RMS prologue's pass-1 loads (one batch: K <= RMS_ONE_BATCH_K), also ahead of the prefetch
     if (kRmsOn) rms_load<kRmsRes>(rb, X, rms.R, 4 * tid, K);
-    // and every gain the quantisation pass will read (its blocks b0 + STEP*i,
-    // clamped), so that pass waits for neither the weight prefetch (vmcnt
-    // retires in order) nor a round trip of its own
-    constexpr int RMS_STEP = RMS_THREADS / 8;
-    constexpr int RMS_Q_ROUNDS = (int)((RMS_ONE_BATCH_K / QK8_1 + RMS_STEP - 1) / RMS_STEP);
-    float gain[RMS_Q_ROUNDS][4];
+    // and the eight gains the quantisation pass will read (block tid/4, eight
+    // elements per lane: one round covers K <= RMS_ONE_BATCH_K), so that pass
+    // waits for neither the weight prefetch (vmcnt retires in order) nor a
+    // round trip of its own
+    static_assert(RMS_ONE_BATCH_K / QK8_1 * 4 <= RMS_THREADS, "one quantisation round per K");
+    const int qe = 8 * min(tid, 4 * nb - 1);  // this lane's first element (clamped: every load unconditional)
+    v4f gain[2];
     if constexpr (kRmsOn && kRmsGain) {
-        const int j = q8_lane_elem(tid & 7);
-#pragma unroll
-        for (int r = 0; r < RMS_Q_ROUNDS; ++r) {
-            const int b = min((tid >> 3) + RMS_STEP * r, nb - 1);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) gain[r][i] = rms.gamma[b * QK8_1 + j + 8 * i];
-        }
+        gain[0] = *reinterpret_cast<const v4f*>(rms.gamma + qe);
+        gain[1] = *reinterpret_cast<const v4f*>(rms.gamma + qe + 4);
     }
     // Every weight load is unconditional (steps past this wave's last one
     // repeat it), so the wait counts are compile-time exact.
@@ -696,23 +692,18 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
         const size_t h_off = ((size_t)K + (size_t)nb * 4 + (size_t)rows_per_wg * bpr * 4 + 15) & ~(size_t)15;
         float* shh = reinterpret_cast<float*>(lds + h_off);
         const double acc = rms_accumulate<kRmsRes, true>(rb, blockIdx.x == 0 ? rms.H : nullptr, shh, 4 * tid, K, 0.0);
-        const int j = q8_lane_elem(tid & 7);
         const float scale = rms_scale(rms_reduce(acc, rms_part, tid), K, rms.eps);
+        if (tid < 4 * nb) {  // uniform per quad: block tid/4, elements qe .. qe+7
+            const v4f h0 = *reinterpret_cast<const v4f*>(shh + qe), h1 = *reinterpret_cast<const v4f*>(shh + qe + 4);
+            float y[8];
 #pragma unroll
-        for (int r = 0; r < RMS_Q_ROUNDS; ++r) {
-            const int b = (tid >> 3) + RMS_STEP * r;
-            if (b < nb) {  // uniform per 8-lane group
-                const int e = b * QK8_1 + j;
-                float y[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) y[i] = rms_y<kRmsGain>(shh[e + 8 * i], scale, kRmsGain ? gain[r][i] : 0.0f);
-                const Q8Block8 q = quantize_block8(y[0], y[1], y[2], y[3]);
-                sq[e] = (int8_t)q.q0;
-                sq[e + 8] = (int8_t)q.q1;
-                sq[e + 16] = (int8_t)q.q2;
-                sq[e + 24] = (int8_t)q.q3;
-                if (j == 0) sdx[b] = half_bits_to_float(q.ds & 0xFFFFu);
+            for (int i = 0; i < 4; ++i) {
+                y[i] = rms_y<kRmsGain>(h0[i], scale, kRmsGain ? gain[0][i] : 0.0f);
+                y[4 + i] = rms_y<kRmsGain>(h1[i], scale, kRmsGain ? gain[1][i] : 0.0f);
             }
+            const Q8Quad q = quantize_quad8(y);
+            *reinterpret_cast<v2u*>(sq + qe) = v2u{q.q_lo, q.q_hi};
+            if ((tid & 3) == 0) sdx[tid >> 2] = half_bits_to_float(q.d_bits);
         }
     } else if (split) {
         fused_store(fx, sq, sdx, tasks, tid, nthreads);

@@ -66,4 +66,32 @@ __device__ inline Q8Block8 quantize_block8(float x0, float x1, float x2, float x
     return out;
 }
 
+// The same block held by four cooperating lanes (an aligned quad), eight
+// consecutive elements each: lane L holds x[8L .. 8L+7].  amax is the max
+// over the quad (DPP quad_perm xor 2, xor 1; max is exact in any order), so
+// d and every code are those of quantize_block8; the block sum is not formed.
+// Returns the eight codes as bytes, x[8L] in the lowest, and rtz-fp16(d).
+struct Q8Quad {
+    uint32_t q_lo, q_hi;  // codes of x[8L .. 8L+3], x[8L+4 .. 8L+7]
+    uint32_t d_bits;      // rtz-fp16(d) (identical in the four lanes)
+};
+
+__device__ inline Q8Quad quantize_quad8(const float (&x)[8]) {
+    float a = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    a = fmaxf(a, fmaxf(fmaxf(fabsf(x[4]), fabsf(x[5])), fmaxf(fabsf(x[6]), fabsf(x[7]))));
+    a = fmaxf(a, dpp_f32<0x4E>(a));  // quad_perm [2,3,0,1]
+    a = fmaxf(a, dpp_f32<0xB1>(a));  // quad_perm [1,0,3,2]
+    const float d = a / 127.0f;
+    Q8Quad out{0u, 0u, float_to_half_bits_rtz(d)};
+    if (a != 0.0f) {
+        const float r = __builtin_amdgcn_rcpf(d);
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = (uint32_t)round_div(x[i], d, r) & 0xFFu;
+        out.q_lo = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+        out.q_hi = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+    }
+    return out;
+}
+
 }  // namespace iq4xs

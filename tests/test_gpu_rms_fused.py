@@ -77,6 +77,7 @@ def test_fused_rejects(pkg, dev):
     yx = P1(X.data_ptr() + 4 * 16)
     assert f(1, wp, yx, nn, X.data_ptr(), None, None, None, 1e-6, K, s) == inv
     assert f(1, wp, yp, nn, X.data_ptr() + 4, None, None, None, 1e-6, K, s) == inv  # unaligned X
+    assert f(1, wp, yp, nn, X.data_ptr(), None, None, X.data_ptr() + 4 * K + 4, 1e-6, K, s) == inv  # unaligned gamma
     # shapes the fused prologue does not take
     Ws = pkg.synthetic_weights(1024, N, seed=2, device=dev)
     assert f(1, P1(Ws.data_ptr()), yp, nn, X.data_ptr(), None, None, None, 1e-6, 1024, s) == nsup
