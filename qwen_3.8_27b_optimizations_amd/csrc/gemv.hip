@@ -673,12 +673,13 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
         gain[1] = *reinterpret_cast<const v4f*>(rms.gamma + qe + 4);
     }
     // Every weight load is unconditional (steps past this wave's last one
-    // repeat it), so the wait counts are compile-time exact.
+    // repeat it; a wave with no step loads the tile's last), so the wait
+    // counts are compile-time exact.  A branch around this prefetch would
+    // make the prologue's own waits count as if it had not been issued
+    // (vmcnt(0): the activations would wait for the weights).
     StepRegs buf[D];
-    if (my_n > 0) {
 #pragma unroll
-        for (int d = 0; d < D - 1; ++d) load(buf[d], wave + TILE_WAVES * min(d, my_n - 1));
-    }
+    for (int d = 0; d < D - 1; ++d) load(buf[d], min(wave + TILE_WAVES * min(d, max(my_n - 1, 0)), last_step));
     // (8*s) mod bpr of this wave's current step, and its advance per own
     // step (64 super-blocks) mod bpr; bpr >= 8, so a few subtractions do.
     int u = 8 * wave;
