@@ -227,6 +227,46 @@ __device__ inline void fused_store(const FusedRegs& r, int8_t* sq, float* sdx, i
     }
 }
 
+// The same prologue for a 16-byte aligned column with unit stride: lane t of
+// an 8-lane group holds elements 4t .. 4t+3 of its block (one 16-byte load;
+// a wave's load covers 1 KB of x, against 64 lines touched by the strided
+// form), amax by three DPP steps over the group (max is exact in any order),
+// then the d and codes of quantize_block8 -- the same bits.
+struct FusedVecRegs {
+    v4f x[FUSED_ROUNDS];
+};
+
+__device__ inline void fused_load_vec(FusedVecRegs& r, const float* __restrict__ X, int tasks, int tid,
+                                      int nthreads) {
+#pragma unroll
+    for (int u = 0; u < FUSED_ROUNDS; ++u)
+        r.x[u] = *reinterpret_cast<const v4f*>(X + 4 * min(tid + u * nthreads, tasks - 1));  // clamped
+}
+
+__device__ inline void fused_store_vec(const FusedVecRegs& r, int8_t* sq, float* sdx, int tasks, int tid,
+                                       int nthreads) {
+#pragma unroll
+    for (int u = 0; u < FUSED_ROUNDS; ++u) {
+        const int t = tid + u * nthreads;
+        if (t < tasks) {  // tasks % 64 == 0: whole 8-lane groups and waves
+            const v4f x = r.x[u];
+            float a = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+            a = fmaxf(a, dpp_f32<0xB1>(a));   // quad_perm [1,0,3,2]
+            a = fmaxf(a, dpp_f32<0x4E>(a));   // quad_perm [2,3,0,1]
+            a = fmaxf(a, dpp_f32<0x141>(a));  // row_half_mirror: lane L <-> 7 - L of the group
+            const float d = a / 127.0f;
+            uint32_t q = 0;
+            if (a != 0.0f) {
+                const float rc = __builtin_amdgcn_rcpf(d);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) q |= ((uint32_t)round_div(x[i], d, rc) & 0xFFu) << (8 * i);
+            }
+            *reinterpret_cast<uint32_t*>(sq + 4 * t) = q;
+            if ((t & 7) == 0) sdx[t >> 3] = half_bits_to_float(float_to_half_bits_rtz(d));
+        }
+    }
+}
+
 // Fused prologue: quantise the fp32 activations (element (c, k) at
 // X[c*sc + k*sk]) straight into LDS, eight lanes per block.  Only d is kept:
 // the dot uses the fp16-truncated d exactly as the planar path does.  Loads of
@@ -579,13 +619,16 @@ struct RmsArgs {
 };
 
 // kRms: 0 = none; bit 0 = the RMS-norm prologue (C == 1), bit 1 = with a
-// residual R, bit 2 = with a gain gamma.
+// residual R, bit 2 = with a gain gamma; bit 4 = the fused single-column
+// quantisation loads x as 16-byte vectors (x 16-byte aligned, unit stride).
 template <int C, int D, bool kDebug, bool kFuse, bool kGroup, int kRms = 0>
 __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const GemvGroup grp, const int8_t* __restrict__ aqs, const uint32_t* __restrict__ ads,
     const float* __restrict__ X, int64_t sc, int64_t sk, int K, int64_t ldy_n, int rows_per_wg,
     int32_t* __restrict__ dbg, const RmsArgs rms) {
     constexpr bool kRmsOn = (kRms & 1) != 0, kRmsRes = (kRms & 2) != 0, kRmsGain = (kRms & 4) != 0;
+    constexpr bool kVecX = (kRms & 16) != 0;
+    static_assert(!kVecX || (kFuse && C == 1 && !kRmsOn), "vector x loads serve the single-column fused prologue");
     static_assert(!kRmsOn || (C == 1 && !kFuse && RMS_THREADS == 64 * TILE_WAVES),
                   "the RMS prologue runs the producer's own 1024-thread reduction on one column");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -658,7 +701,13 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const int tasks = K / 4;
     const bool split = kFuse && C == 1 && tasks <= FUSED_ROUNDS * nthreads;
     FusedRegs fx;
-    if (split) fused_load(fx, X, sk, tasks, tid, nthreads);
+    FusedVecRegs fv;
+    if (split) {
+        if constexpr (kVecX)
+            fused_load_vec(fv, X, tasks, tid, nthreads);
+        else
+            fused_load(fx, X, sk, tasks, tid, nthreads);
+    }
     RmsBatch rb;  // the RMS prologue's pass-1 loads (one batch: K <= RMS_ONE_BATCH_K), also ahead of the prefetch
     if (kRmsOn) rms_load<kRmsRes>(rb, X, rms.R, 4 * tid, K);
     // and the eight gains the quantisation pass will read (block tid/4, eight
@@ -707,7 +756,10 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
             if ((tid & 3) == 0) sdx[tid >> 2] = half_bits_to_float(q.d_bits);
         }
     } else if (split) {
-        fused_store(fx, sq, sdx, tasks, tid, nthreads);
+        if constexpr (kVecX)
+            fused_store_vec(fv, sq, sdx, tasks, tid, nthreads);
+        else
+            fused_store(fx, sq, sdx, tasks, tid, nthreads);
     } else if (kFuse) {
         quantize_to_lds<C>(X, sc, sk, K, sq, sdx, tid, nthreads);
     } else {
@@ -921,7 +973,14 @@ static hipError_t launch_tile_d(const TileMat* mats, int count, const int8_t* aq
         hipLaunchKernelGGL((gemv_tile_kernel<C, D, false, false, true>), grid, block, lds, stream, grp, aqs, ads, X,
                            sc, sk, (int)K, ldy_n, (int)R, dbg, RmsArgs{});
     } else if (X != nullptr) {
-        if (dbg) IQ4XS_LAUNCH_TILE(true, true); else IQ4XS_LAUNCH_TILE(false, true);
+        // unit stride and 16-byte alignment: the prologue's vector loads
+        const bool vec = C == 1 && sk == 1 && reinterpret_cast<uintptr_t>(X) % 16 == 0 &&
+                         (K / 4) <= FUSED_ROUNDS * 64 * TILE_WAVES;
+        if (dbg) IQ4XS_LAUNCH_TILE(true, true);
+        else if (vec)
+            hipLaunchKernelGGL((gemv_tile_kernel<C, D, false, true, false, (C == 1 ? 16 : 0)>), grid, block, lds, stream,
+                               grp, aqs, ads, X, sc, sk, (int)K, ldy_n, (int)R, dbg, RmsArgs{});
+        else IQ4XS_LAUNCH_TILE(false, true);
     } else {
         if (dbg) IQ4XS_LAUNCH_TILE(true, false); else IQ4XS_LAUNCH_TILE(false, false);
     }

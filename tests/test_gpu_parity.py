@@ -245,11 +245,35 @@ def test_fused_quantize_gemv(pkg, orc, dev, K, N, M, layout):
     assert np.array_equal(Sf.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, M))
     if M == 1:
         assert torch.equal(Yf, Yp)
+        assert torch.equal(pkg.mul_mat_fused(Wd, Xd, K, N, M, layout), Yp)  # without the debug store
     else:
         m = compute_metrics(Yp.cpu().numpy(), Yf.cpu().numpy())
         assert m["rel_l2"] <= REL_L2_TOL and not m["bad"], m
     Ymn = Yf.cpu().numpy() if layout == LAYOUT_MK else Yf.cpu().numpy().T
     check_outputs(orc, W, AQ, Ymn, K, N, M, "fused")
+
+
+@pytest.mark.parametrize("K,N", [(5120, 333), (17408, 40)])
+def test_fused_single_column_unaligned_x(pkg, orc, dev, K, N):
+    """A single column whose fp32 activations start 4 bytes past a 16-byte
+    boundary takes the per-element prologue loads instead of the 16-byte
+    vector loads; both must give the two-launch path's bits."""
+    W = orc.gen_weights(K, N, seed=5100 + K + N)
+    X = orc.gen_activations(K, seed=6100, outliers=True).reshape(1, K)
+    AQ = orc.quantize_q8_1_batched(X, K, 1, LAYOUT_MK)
+    Wd = D(W, dev)
+    buf = torch.zeros(K + 4, dtype=torch.float32, device=dev)
+    buf[1:K + 1] = D(X.reshape(K), dev)
+    Xu = buf[1:K + 1]
+    assert Xu.data_ptr() % 16 == 4
+    Yd, Sf = pkg.mul_mat_fused(Wd, Xu, K, N, 1, LAYOUT_MK, sums=True)  # the debug-store instance
+    Yf = pkg.mul_mat_fused(Wd, Xu, K, N, 1, LAYOUT_MK)                   # per-element loads
+    Ya = pkg.mul_mat_fused(Wd, D(X, dev), K, N, 1, LAYOUT_MK)            # 16-byte loads
+    Yp = pkg.mul_mat_q8_1(Wd, pkg.quantize_q8_1(D(X, dev), K, 1, LAYOUT_MK), K, N, 1, LAYOUT_MK, pkg.PATH_GEMV)
+    torch.cuda.synchronize()
+    assert np.array_equal(Sf.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, 1))
+    assert torch.equal(Yd, Yp) and torch.equal(Yf, Yp) and torch.equal(Ya, Yp)
+    check_outputs(orc, W, AQ, Yf.cpu().numpy(), K, N, 1, "fused-unaligned")
 
 
 def test_fused_rejects_oversized_activations(pkg, dev):
