@@ -254,14 +254,11 @@ __device__ inline void fused_store_vec(const FusedVecRegs& r, int8_t* sq, float*
             a = fmaxf(a, dpp_f32<0xB1>(a));   // quad_perm [1,0,3,2]
             a = fmaxf(a, dpp_f32<0x4E>(a));   // quad_perm [2,3,0,1]
             a = fmaxf(a, dpp_f32<0x141>(a));  // row_half_mirror: lane L <-> 7 - L of the group
-            const float d = a / 127.0f;
-            uint32_t q = 0;
-            if (a != 0.0f) {
-                const float rc = __builtin_amdgcn_rcpf(d);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) q |= ((uint32_t)round_div(x[i], d, rc) & 0xFFu) << (8 * i);
-            }
-            *reinterpret_cast<uint32_t*>(sq + 4 * t) = q;
+            const float d = div127(a);
+            const float xs[4] = {x[0], x[1], x[2], x[3]};
+            int q[4];
+            round_codes(xs, a, d, q);
+            *reinterpret_cast<uint32_t*>(sq + 4 * t) = pack_codes4(q[0], q[1], q[2], q[3]);
             if ((t & 7) == 0) sdx[t >> 3] = half_bits_to_float(float_to_half_bits_rtz(d));
         }
     }

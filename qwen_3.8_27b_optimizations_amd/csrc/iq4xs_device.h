@@ -82,10 +82,11 @@ __host__ __device__ inline uint32_t float_to_half_bits_rtz(float f) {
     const uint32_t sign = (x >> 16) & 0x8000u;
     const int e = (int)((x >> 23) & 0xFFu) - 112;  // rebias 127 -> 15
     const uint32_t m10 = (x >> 13) & 0x3FFu;
-    if (e >= 31) return sign | 0x7C00u;
-    if (e > 0) return sign | ((uint32_t)e << 10) | m10;
-    if (e < -10) return sign;
-    return sign | ((m10 | 0x400u) >> (1 - e));
+    // selects, not branches: the subnormal shift 1 - e is clamped to 31, which
+    // also gives the signed zero of e < -10 ((m10 | 0x400) < 2^11)
+    const uint32_t sub = (m10 | 0x400u) >> (1 - e < 0 ? 0 : (1 - e > 31 ? 31 : 1 - e));
+    const uint32_t mag = e >= 31 ? 0x7C00u : (e > 0 ? ((uint32_t)e << 10) | m10 : sub);
+    return sign | mag;
 }
 
 // 6-bit scale of sub-block ib from the first 8 bytes of a super-block

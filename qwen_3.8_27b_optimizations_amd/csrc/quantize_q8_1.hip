@@ -35,17 +35,11 @@ __device__ inline void quantize_block_regs(const float (&x)[32], uint32_t (&q)[8
         }
     }
     const float amax = a[0];
-    const float d = amax / 127.0f;
+    const float d = div127(amax);
+    int c[32];
+    round_codes(x, amax, d, c);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int qi = (amax != 0.0f) ? (int)roundf(x[4 * j + i] / d) : 0;
-            packed |= ((uint32_t)qi & 0xFFu) << (8 * i);
-        }
-        q[j] = packed;
-    }
+    for (int j = 0; j < 8; ++j) q[j] = pack_codes4(c[4 * j], c[4 * j + 1], c[4 * j + 2], c[4 * j + 3]);
     ds = float_to_half_bits_rtz(d) | (float_to_half_bits_rtz(s[0]) << 16);
 }
 
