@@ -66,9 +66,10 @@ int quantize_row_q8_1_gpu(const float* x, void* y, int64_t K, void* stream);
 int quantize_row_q8_1_batched_gpu(const float* X, void* Y, int64_t K, int64_t M, void* stream);
 
 /* Replaces gemv_iq4xs_stock_dp4a_gpu, real_stock_dp4a_comparator.hip:480-503:
- * y[N] = W x (x quantised to Q8_1 first).  For K <= 8192 the quantisation runs
- * inside the GEMV kernel (one launch, no scratch); otherwise the Q8_1 scratch
- * comes from the device's stream-ordered pool (hipMallocAsync/hipFreeAsync on
+ * y[N] = W x (x quantised to Q8_1 first).  For K <= 20480 with x 16-byte
+ * aligned (K <= 8192 otherwise) the quantisation runs inside the GEMV kernel
+ * (one launch, no scratch); otherwise the Q8_1 scratch comes from the
+ * library's stream-ordered pool (hipMallocFromPoolAsync/hipFreeAsync on
  * `stream`): no device-wide synchronisation, unlike the reference's
  * hipMalloc/hipFree. */
 int gemv_iq4xs_stock_dp4a_gpu(const void* W, const float* x, float* y, int64_t K, int64_t N, void* stream);
@@ -241,8 +242,9 @@ int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64
 int iq4xs_mul_mat_q8_1_group(int count, const void* const* W, float* const* Y, const int64_t* N, const void* ws,
                              int64_t K, int64_t M, int layout, void* stream);
 
-/* Quantise + multiply in one call.  For M == 1 and K <= 8192 the quantisation
- * runs inside the GEMV kernel and ws is not written (it is still validated). */
+/* Quantise + multiply in one call.  For M == 1 and K <= 20480 with X 16-byte
+ * aligned (K <= 8192 otherwise) the quantisation runs inside the GEMV kernel
+ * and ws is not written (it is still validated). */
 int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout, void* ws,
                   size_t ws_bytes, void* stream);
 

@@ -116,23 +116,29 @@ hipError_t mul_mat_planar(const uint8_t* W, const void* ws, float* Y, int64_t K,
     return hipErrorInvalidValue;
 }
 
-// Single-column calls with K up to this bound run the GEMV with the Q8_1
+// Single-column calls with K up to these bounds run the GEMV with the Q8_1
 // quantisation in its prologue (one launch, no workspace).  Every workgroup
-// quantises the whole column, so the prologue grows with K: past this bound
-// (and for M > 1) a separate quantiser launch is cheaper (measured on the
-// decode set with one 16-wave workgroup per CU: 8192 ahead of 6144 and of
-// 17408).
+// quantises the whole column, so the prologue grows with K.  A 16-byte
+// aligned column is loaded as vectors and quantised in up to five rounds: it
+// fuses up to K = 20480 (measured on the decode set: down_proj, K = 17408,
+// 0.6 us per layer faster fused).  Other columns take per-element loads in at
+// most two rounds: up to K = 8192 (measured: 8192 ahead of 6144 and of 17408).
+// Past the bound (and for M > 1) a separate quantiser launch is cheaper.
 constexpr int64_t FUSED_MAX_K = 8192;
 
-int64_t fused_max_k() {
+int64_t fused_max_k_override() {
     static const int64_t v = []() -> int64_t {
-        const char* e = getenv("IQ4XS_FUSED_MAX_K");  // tuning override
-        return e ? atoll(e) : FUSED_MAX_K;
+        const char* e = getenv("IQ4XS_FUSED_MAX_K");  // tuning override of both bounds
+        return e ? atoll(e) : -1;
     }();
     return v;
 }
 
-bool prefer_fused(int64_t K, int64_t M) { return M == 1 && K <= fused_max_k(); }
+bool prefer_fused(int64_t K, int64_t M, const float* X) {
+    const int64_t o = fused_max_k_override();
+    const int64_t bound = o >= 0 ? o : (reinterpret_cast<uintptr_t>(X) % 16 == 0 ? GEMV_FUSED_VEC_MAX_K : FUSED_MAX_K);
+    return M == 1 && K <= bound;
+}
 
 hipError_t mul_mat_fused(const uint8_t* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
                          int32_t* dbg, hipStream_t stream) {
@@ -147,7 +153,7 @@ hipError_t mul_mat_fused(const uint8_t* W, const float* X, float* Y, int64_t K, 
 hipError_t mul_mat_pooled(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M, int layout,
                           hipStream_t stream) {
     if (!valid_mat(W, X, Y, K, N, M)) return hipErrorInvalidValue;
-    if (prefer_fused(K, M)) {
+    if (prefer_fused(K, M, X)) {
         const hipError_t e = mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, nullptr, stream);
         if (e != hipErrorNotSupported) return e;
     }
@@ -332,7 +338,7 @@ int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N,
     if (!valid_mat(W, X, Y, K, N, M) || !ws) return hipErrorInvalidValue;
     if ((layout != LAYOUT_KM && layout != LAYOUT_MK) || ws_bytes < planar_bytes(K, M)) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return hipErrorInvalidValue;
-    if (prefer_fused(K, M)) {
+    if (prefer_fused(K, M, X)) {
         const hipError_t e =
             mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, nullptr, as_stream(stream));
         if (e != hipErrorNotSupported) return e;
@@ -355,7 +361,7 @@ int iq4xs_mul_mat_noalloc(const void* W, const float* X, float* Y, int64_t K, in
     hipError_t err = noalloc_scratch(&ws);
     if (err != hipSuccess) return err;
     hipStream_t s = as_stream(stream);
-    if (prefer_fused(K, M)) {
+    if (prefer_fused(K, M, X)) {
         const hipError_t e = mul_mat_fused(static_cast<const uint8_t*>(W), X, Y, K, N, M, layout, nullptr, s);
         if (e != hipErrorNotSupported) return e;
     }

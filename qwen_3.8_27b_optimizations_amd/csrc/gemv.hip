@@ -193,6 +193,7 @@ __device__ inline void stage_activations(const int8_t* __restrict__ aqs, const u
 // two or more of them repeats at K <= 8192, measured 2 % slower on the bs=1
 // decode step.  Needs K/4 <= 2 * threads (longer rows take quantize_to_lds).
 constexpr int FUSED_ROUNDS = 2;
+constexpr int FUSED_VEC_ROUNDS_LONG = 5;  // the vector prologue up to K = 20480
 struct FusedRegs {
     float x[FUSED_ROUNDS][4];
 };
@@ -232,21 +233,24 @@ __device__ inline void fused_store(const FusedRegs& r, int8_t* sq, float* sdx, i
 // a wave's load covers 1 KB of x, against 64 lines touched by the strided
 // form), amax by three DPP steps over the group (max is exact in any order),
 // then the d and codes of quantize_block8 -- the same bits.
+template <int ROUNDS>
 struct FusedVecRegs {
-    v4f x[FUSED_ROUNDS];
+    v4f x[ROUNDS];
 };
 
-__device__ inline void fused_load_vec(FusedVecRegs& r, const float* __restrict__ X, int tasks, int tid,
+template <int ROUNDS>
+__device__ inline void fused_load_vec(FusedVecRegs<ROUNDS>& r, const float* __restrict__ X, int tasks, int tid,
                                       int nthreads) {
 #pragma unroll
-    for (int u = 0; u < FUSED_ROUNDS; ++u)
+    for (int u = 0; u < ROUNDS; ++u)
         r.x[u] = *reinterpret_cast<const v4f*>(X + 4 * min(tid + u * nthreads, tasks - 1));  // clamped
 }
 
-__device__ inline void fused_store_vec(const FusedVecRegs& r, int8_t* sq, float* sdx, int tasks, int tid,
+template <int ROUNDS>
+__device__ inline void fused_store_vec(const FusedVecRegs<ROUNDS>& r, int8_t* sq, float* sdx, int tasks, int tid,
                                        int nthreads) {
 #pragma unroll
-    for (int u = 0; u < FUSED_ROUNDS; ++u) {
+    for (int u = 0; u < ROUNDS; ++u) {
         const int t = tid + u * nthreads;
         if (t < tasks) {  // tasks % 64 == 0: whole 8-lane groups and waves
             const v4f x = r.x[u];
@@ -593,6 +597,7 @@ __global__ __launch_bounds__(64 * FLAT_WAVES) void gemv_flat_kernel(
 // workgroups stage (or, fused, quantise) the activations (graph-replayed
 // decode set: fused step +5.5 %, prequantised +1.5 %, bs = 2 +4.5 %).
 constexpr int TILE_WAVES = 16;
+static_assert(4 * FUSED_VEC_ROUNDS_LONG * 64 * TILE_WAVES == GEMV_FUSED_VEC_MAX_K, "vector prologue bound");
 
 // Up to GEMV_GROUP_MAX weight matrices with the same K that read the same
 // activations, run by one launch: matrix g owns tiles [tile_end[g-1],
@@ -625,6 +630,7 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     int32_t* __restrict__ dbg, const RmsArgs rms) {
     constexpr bool kRmsOn = (kRms & 1) != 0, kRmsRes = (kRms & 2) != 0, kRmsGain = (kRms & 4) != 0;
     constexpr bool kVecX = (kRms & 16) != 0;
+    constexpr int kVecRounds = (kRms & 32) ? FUSED_VEC_ROUNDS_LONG : FUSED_ROUNDS;
     static_assert(!kVecX || (kFuse && C == 1 && !kRmsOn), "vector x loads serve the single-column fused prologue");
     static_assert(!kRmsOn || (C == 1 && !kFuse && RMS_THREADS == 64 * TILE_WAVES),
                   "the RMS prologue runs the producer's own 1024-thread reduction on one column");
@@ -696,9 +702,9 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     // staged after the prefetch, below).
     const int nthreads = blockDim.x;
     const int tasks = K / 4;
-    const bool split = kFuse && C == 1 && tasks <= FUSED_ROUNDS * nthreads;
+    const bool split = kFuse && C == 1 && tasks <= (kVecX ? kVecRounds : FUSED_ROUNDS) * nthreads;
     FusedRegs fx;
-    FusedVecRegs fv;
+    FusedVecRegs<kVecRounds> fv;
     if (split) {
         if constexpr (kVecX)
             fused_load_vec(fv, X, tasks, tid, nthreads);
@@ -971,11 +977,13 @@ static hipError_t launch_tile_d(const TileMat* mats, int count, const int8_t* aq
                            sc, sk, (int)K, ldy_n, (int)R, dbg, RmsArgs{});
     } else if (X != nullptr) {
         // unit stride and 16-byte alignment: the prologue's vector loads
-        const bool vec = C == 1 && sk == 1 && reinterpret_cast<uintptr_t>(X) % 16 == 0 &&
-                         (K / 4) <= FUSED_ROUNDS * 64 * TILE_WAVES;
+        const bool vec = C == 1 && sk == 1 && reinterpret_cast<uintptr_t>(X) % 16 == 0;
         if (dbg) IQ4XS_LAUNCH_TILE(true, true);
-        else if (vec)
+        else if (vec && (K / 4) <= FUSED_ROUNDS * 64 * TILE_WAVES)
             hipLaunchKernelGGL((gemv_tile_kernel<C, D, false, true, false, (C == 1 ? 16 : 0)>), grid, block, lds, stream,
+                               grp, aqs, ads, X, sc, sk, (int)K, ldy_n, (int)R, dbg, RmsArgs{});
+        else if (vec && (K / 4) <= FUSED_VEC_ROUNDS_LONG * 64 * TILE_WAVES)
+            hipLaunchKernelGGL((gemv_tile_kernel<C, D, false, true, false, (C == 1 ? 48 : 0)>), grid, block, lds, stream,
                                grp, aqs, ads, X, sc, sk, (int)K, ldy_n, (int)R, dbg, RmsArgs{});
         else IQ4XS_LAUNCH_TILE(false, true);
     } else {

@@ -23,6 +23,9 @@ constexpr int LAYOUT_MK = 1;  // X[m*K+k], Y[m*N+n]   (ggml src1 / dst)
 // Largest column count served by the streaming GEMV; wider batches go to the
 // MFMA GEMM.
 constexpr int GEMV_MAX_COLS = 8;
+// Largest K whose single-column fused GEMV prologue takes the 16-byte vector
+// loads (16-byte aligned x): five rounds of 1024 lanes x 4 elements.
+constexpr int64_t GEMV_FUSED_VEC_MAX_K = 20480;
 
 // Planar writers fill all three parts (qs, ds, hq) when qs is non-null.
 hipError_t launch_quantize(const float* X, int64_t K, int64_t M, int layout, int8_t* qs, uint32_t* ds, uint32_t* hq,

@@ -253,7 +253,7 @@ def test_fused_quantize_gemv(pkg, orc, dev, K, N, M, layout):
     check_outputs(orc, W, AQ, Ymn, K, N, M, "fused")
 
 
-@pytest.mark.parametrize("K,N", [(5120, 333), (17408, 40)])
+@pytest.mark.parametrize("K,N", [(5120, 333), (17408, 40), (20480, 17)])
 def test_fused_single_column_unaligned_x(pkg, orc, dev, K, N):
     """A single column whose fp32 activations start 4 bytes past a 16-byte
     boundary takes the per-element prologue loads instead of the 16-byte
@@ -270,9 +270,14 @@ def test_fused_single_column_unaligned_x(pkg, orc, dev, K, N):
     Yf = pkg.mul_mat_fused(Wd, Xu, K, N, 1, LAYOUT_MK)                   # per-element loads
     Ya = pkg.mul_mat_fused(Wd, D(X, dev), K, N, 1, LAYOUT_MK)            # 16-byte loads
     Yp = pkg.mul_mat_q8_1(Wd, pkg.quantize_q8_1(D(X, dev), K, 1, LAYOUT_MK), K, N, 1, LAYOUT_MK, pkg.PATH_GEMV)
+    # the public entry: an aligned column fuses up to K = 20480, an unaligned one
+    # up to K = 8192 (past it: quantiser launch + GEMV); the same bits either way
+    Ym = pkg.mul_mat(Wd, D(X, dev), K, N, 1, LAYOUT_MK)
+    Ymu = pkg.mul_mat(Wd, Xu, K, N, 1, LAYOUT_MK)
     torch.cuda.synchronize()
     assert np.array_equal(Sf.cpu().numpy(), orc.subblock_sums(W, AQ, K, N, 1))
     assert torch.equal(Yd, Yp) and torch.equal(Yf, Yp) and torch.equal(Ya, Yp)
+    assert torch.equal(Ym, Yp) and torch.equal(Ymu, Yp)
     check_outputs(orc, W, AQ, Yf.cpu().numpy(), K, N, 1, "fused-unaligned")
 
 
