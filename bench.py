@@ -7,9 +7,11 @@ as its own call of the C ABI (fp32 activations in, fp32 outputs out: the Q8_1
 quantisation is part of the call).  One step = the seven projections of one
 layer.  `--layers` distinct layer copies (default 16 = 3.07 GB of IQ4_XS) are
 generated on the device and rotated, so the 256 MB Infinity Cache cannot
-serve repeats: every step streams its weights from HBM.  Each layer copy's
-step is captured into a HIP graph of its own; exactly --warmup untimed and
-then --steps timed steps are replayed in rotation order.
+serve repeats: every step streams its weights from HBM.  Consecutive steps
+walk the copies in rotation order; the --warmup untimed steps and then the
+--steps timed steps are each captured as HIP graphs of up to 64 consecutive
+steps (calls back to back, as a decode chain captures its layers) and
+replayed, so exactly that many steps run.
 
 value     algorithmic bytes per step (sum of N*K*136/256 + 4K + 4N over the
           seven GEMVs) / time per step.
@@ -480,37 +482,47 @@ def main() -> int:
     del gr_run
 
     # ---- headline: whole steps (quantise + GEMV per projection) ------------
-    # One graph per step (the seven calls of one layer copy), replayed in
-    # rotation order, so exactly --warmup untimed and --steps timed steps run.
-    # Capturing replays each graph once: that priming pass over the 16 copies
-    # is set-up, not warm-up.  The legs above have already kept the GPU busy
-    # for ~0.1 s, so the clocks have settled before the timed region.
-    def step_fn(l):
-        def step() -> None:
-            for i, (_, K, N) in enumerate(SHAPES):
-                L.check("iq4xs_mul_mat", layers[l][i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), K, N, 1,
-                        pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
-        return step
+    # A step is the seven calls of one layer copy; consecutive steps walk the
+    # 16 copies in rotation order.  The warm-up steps and the timed steps are
+    # each captured as graphs of up to GRAPH_STEPS consecutive steps (the calls
+    # back to back, as a decode chain captures its layers), so exactly --warmup
+    # untimed and --steps timed steps run and no graph-launch boundary falls
+    # between two steps except every GRAPH_STEPS.  Capturing runs each graph
+    # once first: that priming pass is set-up, not warm-up.  The legs above
+    # have already kept the GPU busy for ~0.1 s, so the clocks have settled
+    # before the timed region.
+    GRAPH_STEPS = 64
 
-    step_runs = []
-    for l in range(args.layers):
-        fn, launch = capture(torch, stream, step_fn(l), use_graph)
-        step_runs.append(fn)
-    cursor = [0]
+    def steps_fn(first: int, count: int):
+        def run() -> None:
+            for j in range(count):
+                l = (first + j) % args.layers
+                for i, (_, K, N) in enumerate(SHAPES):
+                    L.check("iq4xs_mul_mat", layers[l][i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), K, N, 1,
+                            pkg.LAYOUT_MK, wss[i].data_ptr(), wss[i].numel(), s)
+        return run
 
-    def next_step() -> None:
-        step_runs[cursor[0] % args.layers]()
-        cursor[0] += 1
+    def step_graphs(first: int, count: int):
+        caps = [capture(torch, stream, steps_fn(first + c0, min(GRAPH_STEPS, count - c0)), use_graph)
+                for c0 in range(0, count, GRAPH_STEPS)]
 
-    if args.warmup > 0:
-        timer(next_step, args.warmup)
-    us_total = timer(next_step, args.steps)
+        def run_all() -> None:
+            for r, _ in caps:
+                r()
+        return run_all, caps[-1][1]
+
+    warm_run = step_graphs(0, args.warmup)[0] if args.warmup > 0 else None
+    timed_run, launch = step_graphs(args.warmup, args.steps)
+    if warm_run is not None:
+        timer(warm_run, 1)
+    us_total = timer(timed_run, 1)
     ms_per_step = us_total / args.steps / 1e3
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    # spread: each sample times one rotation of back-to-back steps (one step alone would
-    # also time the idle gap before its graph starts), divided by the steps in it
-    step_stats = spread([timer(next_step, args.layers) / args.layers / 1e3 for _ in range(args.repeats)],
-                        "ms_per_step")
+    del warm_run, timed_run
+    # spread: each sample times one rotation of back-to-back steps (one graph)
+    rot_run = step_graphs(0, args.layers)[0]
+    step_stats = spread([timer(rot_run, 1) / args.layers / 1e3 for _ in range(args.repeats)], "ms_per_step")
+    del rot_run
 
     if args.copy_probe:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device=dev)
