@@ -220,8 +220,11 @@ class ModelChain:
     variant "grouped" runs q,k,v and gate,up as one iq4xs_mul_mat_q8_1_group
     launch each; "fused" (M = 1) runs each rms norm and the group after it as
     one iq4xs_rms_norm_mul_mat_group launch, which writes h into the other of
-    two buffers (it has no in-place form).  Every variant computes the same
-    bits.  The norm gains are 1/1145 so that the synthetic weights (rms ~16
+    two buffers (it has no in-place form); "fused_swiglu" (M = 1) is "fused"
+    with the FFN's norm, gate/up and SwiGLU as one
+    iq4xs_rms_norm_mul_mat_swiglu launch writing S = silu(gate) * up in fp32,
+    and down as iq4xs_mul_mat on S (the quantiser in the GEMV's prologue):
+    four launches per layer.  Every variant computes the same bits.  The norm gains are 1/1145 so that the synthetic weights (rms ~16
     per element) keep every activation well inside the fp16 range of the Q8_1
     scale.
 
@@ -234,7 +237,7 @@ class ModelChain:
     def __init__(self, torch, pkg, L, weights, M: int, stream, variant: str = "plain", seed: int = 700):
         import ctypes
 
-        assert variant in ("plain", "grouped", "fused") and (variant != "fused" or M == 1)
+        assert variant in ("plain", "grouped", "fused", "fused_swiglu") and (variant in ("plain", "grouped") or M == 1)
         self.torch, self.pkg, self.L, self.weights, self.M, self.variant = torch, pkg, L, weights, M, variant
         self.s = stream.cuda_stream
         dev = weights[0][0].device
@@ -242,6 +245,7 @@ class ModelChain:
         self.gain = torch.full((self.H_DIM,), MODEL_GAIN, device=dev)
         self.h = pkg.synthetic_activations(M * self.H_DIM, seed=seed, device=dev)
         self.h_alt = torch.empty_like(self.h)  # the fused norm writes h into the other buffer
+        self.S = torch.empty((M, SHAPES[4][2]), device=dev)  # fused_swiglu: silu(gate) * up
         self.bufs = {name: torch.zeros((M, N), device=dev) for name, _, N in SHAPES}
         self.wsA = torch.empty(L.iq4xs_workspace_bytes(self.H_DIM, M), dtype=torch.uint8, device=dev)
         self.wsB = torch.empty(L.iq4xs_workspace_bytes(self.Q_DIM, M), dtype=torch.uint8, device=dev)
@@ -284,7 +288,7 @@ class ModelChain:
 
         # attention norm -> q, k, v
         h_in, r_in = snap(self.h), snap(b["down_proj"])
-        if self.variant == "fused":  # h + down_prev -> h_alt, norm, q/k/v: one launch
+        if self.variant in ("fused", "fused_swiglu"):  # h + down_prev -> h_alt, norm, q/k/v: one launch
             self._rms_group(l, 0, self.h, b["down_proj"], self.h_alt)
             done("rms_qkv_fused", h_in=h_in, r_in=r_in, h_out=self.h_alt, q=b["q_proj"], k=b["k_proj"],
                  v=b["v_proj"])
@@ -303,6 +307,18 @@ class ModelChain:
                      SHAPES[3][2], self.M, self.pkg.LAYOUT_MK, self.wsB.data_ptr(), self.wsB.numel(), self.s)
         done("o", x=b["q_proj"], o=b["o_proj"])
         # FFN norm -> gate, up
+        if self.variant == "fused_swiglu":  # h_alt + o -> h, norm, gate/up, S = silu(gate) * up: one launch
+            h_in, r_in = snap(self.h_alt), snap(b["o_proj"])
+            self.L.check("iq4xs_rms_norm_mul_mat_swiglu", Wl[4].data_ptr(), Wl[5].data_ptr(), self.FF_DIM,
+                         self.h_alt.data_ptr(), b["o_proj"].data_ptr(), self.h.data_ptr(), self.gain.data_ptr(),
+                         MODEL_EPS, self.H_DIM, b["gate_proj"].data_ptr(), b["up_proj"].data_ptr(),
+                         self.S.data_ptr(), self.s)
+            done("rms_gate_up_swiglu", h_in=h_in, r_in=r_in, h_out=self.h, gate=b["gate_proj"], up=b["up_proj"],
+                 s=self.S)
+            self.L.check("iq4xs_mul_mat", Wl[6].data_ptr(), self.S.data_ptr(), b["down_proj"].data_ptr(), self.FF_DIM,
+                         SHAPES[6][2], self.M, self.pkg.LAYOUT_MK, self.wsC.data_ptr(), self.wsC.numel(), self.s)
+            done("down_from_s", x=self.S, down=b["down_proj"])
+            return
         if self.variant == "fused":  # h_alt + o -> h, norm, gate/up: one launch
             h_in, r_in = snap(self.h_alt), snap(b["o_proj"])
             self._rms_group(l, 1, self.h_alt, b["o_proj"], self.h)
@@ -334,7 +350,8 @@ class ModelChain:
 
     def finite(self) -> bool:
         self.torch.cuda.synchronize()
-        ts = self.state() + ([self.h_alt] if self.variant == "fused" else [])
+        ts = self.state() + ([self.h_alt] if self.variant in ("fused", "fused_swiglu") else [])
+        ts += [self.S] if self.variant == "fused_swiglu" else []
         return all(bool(self.torch.isfinite(t).all()) for t in ts)
 
 
@@ -353,8 +370,12 @@ def model_stream(torch, pkg, L, stream, timer, args, use_graph) -> dict:
     notes = {"bs1": None,
              "bs1_grouped": "same chain; q,k,v and gate,up each one iq4xs_mul_mat_q8_1_group launch",
              "bs1_rms_fused": "same chain; each rms norm and the q,k,v / gate,up group after it are one "
-                              "iq4xs_rms_norm_mul_mat_group launch"}
-    for key, variant in (("bs1", "plain"), ("bs1_grouped", "grouped"), ("bs1_rms_fused", "fused")):
+                              "iq4xs_rms_norm_mul_mat_group launch",
+             "bs1_rms_swiglu_fused": "same chain; as bs1_rms_fused, with the FFN's norm, gate/up and swiglu one "
+                                     "iq4xs_rms_norm_mul_mat_swiglu launch (fp32 silu(gate)*up) and down quantising "
+                                     "it in its prologue: 4 launches per layer"}
+    for key, variant in (("bs1", "plain"), ("bs1_grouped", "grouped"), ("bs1_rms_fused", "fused"),
+                         ("bs1_rms_swiglu_fused", "fused_swiglu")):
         chain = ModelChain(torch, pkg, L, weights, 1, stream, variant)
         run, launch = capture(torch, stream, chain.run, use_graph)
         timer(run, 2)

@@ -221,6 +221,25 @@ int iq4xs_swiglu_q8_1(const float* G, const float* U, int64_t K, int64_t M, void
 int iq4xs_rms_norm_mul_mat_group(int count, const void* const* W, float* const* Y, const int64_t* N, const float* X,
                                  const float* R, float* H, const float* gamma, float eps, int64_t K, void* stream);
 
+/* RMS norm, the gate/up pair of a SwiGLU MLP and the SwiGLU itself in one bs=1
+ * launch: the same h, gate and up as iq4xs_rms_norm_mul_mat_group(2,
+ * {W_gate, W_up}, {Y_gate, Y_up}, {N, N}, X, R, H, gamma, eps, K) -- bit for
+ * bit -- and S[n] = silu(gate[n]) * up[n] in fp32 with iq4xs_swiglu_q8_1's
+ * arithmetic, so iq4xs_mul_mat(W_down, S, ...) gives the bits of the SwiGLU
+ * producer followed by the down GEMV, one launch earlier.  Each workgroup
+ * owns the same rows of gate and up.  No counterpart in the reference, which
+ * runs RMS_NORM, MUL, the two projections and SWIGLU as separate ggml ops.
+ *   - Y_gate, Y_up may be NULL (not written); S must not be NULL;
+ *   - H (may be NULL) must not overlap X or R; Y_gate, Y_up and S must not
+ *     overlap X, R, H or each other;
+ *   - X, R, H, gamma 16-byte aligned; K % 256 == 0, eps >= 0;
+ *   - hipErrorNotSupported as iq4xs_rms_norm_mul_mat_group, or when N has no
+ *     divisor that makes every workgroup's rows whole steps: use the group
+ *     call and iq4xs_swiglu_q8_1. */
+int iq4xs_rms_norm_mul_mat_swiglu(const void* W_gate, const void* W_up, int64_t N, const float* X, const float* R,
+                                  float* H, const float* gamma, float eps, int64_t K, float* Y_gate, float* Y_up,
+                                  float* S, void* stream);
+
 /* Y = W * dequant(ws) from an already quantised workspace; `layout` selects
  * the Y layout; `path` is one of IQ4XS_PATH_*. */
 int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64_t N, int64_t M, int layout,

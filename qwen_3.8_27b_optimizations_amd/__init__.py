@@ -75,6 +75,7 @@ SIGNATURES = {
     "iq4xs_rms_norm_q8_1": (_INT, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, _P, ctypes.c_size_t, _P]),
     "iq4xs_swiglu_q8_1": (_INT, [_P, _P, _I64, _I64, _P, ctypes.c_size_t, _P]),
     "iq4xs_rms_norm_mul_mat_group": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, ctypes.c_float, _I64, _P]),
+    "iq4xs_rms_norm_mul_mat_swiglu": (_INT, [_P, _P, _I64, _P, _P, _P, _P, ctypes.c_float, _I64, _P, _P, _P, _P]),
     "iq4xs_q8_1_to_blocks": (_INT, [_P, _P, _I64, _I64, _P]),
     "iq4xs_subblock_sums": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "iq4xs_probe_mfma_i8": (_INT, [_P, _P, _P, _P]),
@@ -194,6 +195,24 @@ def rms_norm_mul_mat_group(Ws, X, K: int, Ns, residual=None, out_h=None, gamma=N
     lib().check("iq4xs_rms_norm_mul_mat_group", n, wp, yp, nn, X.data_ptr(), ptr(residual), ptr(out_h), ptr(gamma),
                 eps, K, _stream(torch))
     return outs
+
+
+def rms_norm_mul_mat_swiglu(W_gate, W_up, X, K: int, N: int, residual=None, out_h=None, gamma=None,
+                            eps: float = 1e-6, gate_out=None, up_out=None, keep_gate_up: bool = True, out=None):
+    """RMS norm + gate/up GEMVs + SwiGLU in one bs=1 launch: returns (S, gate, up) with S = silu(gate) * up
+    (fp32, the SwiGLU producer's arithmetic); gate/up bit-identical to rms_norm_mul_mat_group on the pair.
+    With keep_gate_up=False gate and up are not written (None is returned for them)."""
+    torch = _torch()
+    _check_weights(W_gate, K, N)
+    _check_weights(W_up, K, N)
+    new = lambda: torch.empty(N, dtype=torch.float32, device=X.device)
+    S = new() if out is None else out
+    g = (new() if gate_out is None else gate_out) if keep_gate_up else None
+    u = (new() if up_out is None else up_out) if keep_gate_up else None
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    lib().check("iq4xs_rms_norm_mul_mat_swiglu", W_gate.data_ptr(), W_up.data_ptr(), N, X.data_ptr(), ptr(residual),
+                ptr(out_h), ptr(gamma), eps, K, ptr(g), ptr(u), S.data_ptr(), _stream(torch))
+    return S, g, u
 
 
 def q8_1_blocks(ws, K: int, M: int):

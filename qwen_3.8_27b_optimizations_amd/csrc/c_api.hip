@@ -432,6 +432,26 @@ int iq4xs_rms_norm_mul_mat_group(int count, const void* const* W, float* const* 
     return launch_gemv_rms_group(count, Wb, Y, N, X, R, H, gamma, eps, K, as_stream(stream));
 }
 
+int iq4xs_rms_norm_mul_mat_swiglu(const void* W_gate, const void* W_up, int64_t N, const float* X, const float* R,
+                                  float* H, const float* gamma, float eps, int64_t K, float* Y_gate, float* Y_up,
+                                  float* S, void* stream) {
+    if (!W_gate || !W_up || !X || !S || !valid_k(K) || K >= MAX_DIM || N <= 0 || N >= MAX_DIM)
+        return hipErrorInvalidValue;
+    if (!(eps >= 0.0f) || !aligned16(X) || !aligned16(R) || !aligned16(H) || !aligned16(gamma))
+        return hipErrorInvalidValue;
+    const size_t bytes = (size_t)K * sizeof(float), yb = (size_t)N * sizeof(float);
+    if (overlaps(H, bytes, X, bytes) || overlaps(H, bytes, R, bytes)) return hipErrorInvalidValue;
+    float* const outs[3] = {Y_gate, Y_up, S};
+    for (int i = 0; i < 3; ++i) {
+        if (overlaps(outs[i], yb, X, bytes) || overlaps(outs[i], yb, R, bytes) || overlaps(outs[i], yb, H, bytes))
+            return hipErrorInvalidValue;
+        for (int j = 0; j < i; ++j)
+            if (overlaps(outs[i], yb, outs[j], yb)) return hipErrorInvalidValue;
+    }
+    return launch_gemv_rms_swiglu(static_cast<const uint8_t*>(W_gate), static_cast<const uint8_t*>(W_up), Y_gate,
+                                  Y_up, S, N, X, R, H, gamma, eps, K, as_stream(stream));
+}
+
 int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, void* stream) {
     if (!ws || !blocks || K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return hipErrorInvalidValue;
     const Planar p = planar_view(ws, K, M);

@@ -31,6 +31,7 @@
 #include <numeric>
 #include <stdlib.h>
 
+#include "act_device.h"
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
 #include "q8_1_block.h"
@@ -612,17 +613,24 @@ struct GemvGroup {
 };
 
 // Arguments of the fused RMS-norm prologue (kRms): h = X (+ R), written to H
-// by workgroup 0 only; the Q8_1 codes of (h * scale) * gamma go to LDS.
+// by workgroup 0 only; the Q8_1 codes of (h * scale) * gamma go to LDS.  With
+// the SwiGLU epilogue, S receives silu(gate) * up of the tile's rows.
 struct RmsArgs {
     const float* R;
     float* H;
     const float* gamma;
     float eps;
+    float* S;
 };
 
 // kRms: 0 = none; bit 0 = the RMS-norm prologue (C == 1), bit 1 = with a
 // residual R, bit 2 = with a gain gamma; bit 4 = the fused single-column
-// quantisation loads x as 16-byte vectors (x 16-byte aligned, unit stride).
+// quantisation loads x as 16-byte vectors (x 16-byte aligned, unit stride),
+// bit 5 = in up to five rounds; bit 6 = the SwiGLU pair: the tile is the
+// same rows_per_wg rows of two matrices, gate (grp.W[0] -> grp.Y[0]) then up
+// (grp.W[1] -> grp.Y[1]), streamed as one run of steps, and the epilogue
+// also writes S = silu(gate) * up for those rows (the host makes every tile
+// whole: rows_per_wg divides N and a tile's gate part fills whole steps).
 template <int C, int D, bool kDebug, bool kFuse, bool kGroup, int kRms = 0>
 __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const GemvGroup grp, const int8_t* __restrict__ aqs, const uint32_t* __restrict__ ads,
@@ -631,6 +639,8 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     constexpr bool kRmsOn = (kRms & 1) != 0, kRmsRes = (kRms & 2) != 0, kRmsGain = (kRms & 4) != 0;
     constexpr bool kVecX = (kRms & 16) != 0;
     constexpr int kVecRounds = (kRms & 32) ? FUSED_VEC_ROUNDS_LONG : FUSED_ROUNDS;
+    constexpr bool kSwi = (kRms & 64) != 0;
+    static_assert(!kSwi || (kRmsOn && !kGroup), "the SwiGLU epilogue serves the rms-fused gate/up pair");
     static_assert(!kVecX || (kFuse && C == 1 && !kRmsOn), "vector x loads serve the single-column fused prologue");
     static_assert(!kRmsOn || (C == 1 && !kFuse && RMS_THREADS == 64 * TILE_WAVES),
                   "the RMS prologue runs the producer's own 1024-thread reduction on one column");
@@ -677,10 +687,13 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     }
     const int r0 = (bid - tile0) * rows_per_wg;
     const int nrows = min(rows_per_wg, N - r0);
-    const int n_sb = nrows * bpr;
+    const int n_sb = (kSwi ? 2 : 1) * nrows * bpr;  // SwiGLU pair: the gate rows, then the same up rows
     const int n_steps = (n_sb + 7) >> 3;
     const int my_n = wave < n_steps ? (n_steps - wave + TILE_WAVES - 1) / TILE_WAVES : 0;
     const uint8_t* Wg = W + (size_t)r0 * bpr * BLOCK_BYTES;
+    // SwiGLU pair: steps from up_step on read the up matrix (wave-uniform select)
+    const int up_step = kSwi ? (nrows * bpr) >> 3 : n_steps;
+    const uint8_t* Wu = kSwi ? grp.W[1] + (size_t)r0 * bpr * BLOCK_BYTES : Wg;
 
     // Only a matrix's last tile can end inside a step: there the lanes past
     // the end re-read the last super-block and are not accumulated.
@@ -690,7 +703,8 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     const uint32_t off_l = (uint32_t)min(slot, last_slot) * BLOCK_BYTES;
     const uint32_t off_q = 16u * (uint32_t)ib;
     auto load = [&](StepRegs& r, int s) {
-        const uint8_t* base = Wg + (size_t)s * (8 * BLOCK_BYTES);  // scalar
+        const bool up = kSwi && s >= up_step;
+        const uint8_t* base = (up ? Wu : Wg) + (size_t)(up ? s - up_step : s) * (8 * BLOCK_BYTES);  // scalar
         const uint32_t o = s == last_step ? off_l : off_n;
         r.h = *reinterpret_cast<const v2u*>(base + o);
         r.q = *reinterpret_cast<const v4i_a8*>(base + (o + off_q) + 8);
@@ -742,7 +756,8 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
         // the producer's passes (rms_device.h), with h staged in LDS after the
         // partials and the codes written straight to the GEMV's LDS operand
         __shared__ double rms_part[RMS_WAVES];
-        const size_t h_off = ((size_t)K + (size_t)nb * 4 + (size_t)rows_per_wg * bpr * 4 + 15) & ~(size_t)15;
+        const size_t h_off =
+            ((size_t)K + (size_t)nb * 4 + (size_t)(kSwi ? 2 : 1) * rows_per_wg * bpr * 4 + 15) & ~(size_t)15;
         float* shh = reinterpret_cast<float*>(lds + h_off);
         const double acc = rms_accumulate<kRmsRes, true>(rb, blockIdx.x == 0 ? rms.H : nullptr, shh, 4 * tid, K, 0.0);
         const float scale = rms_scale(rms_reduce(acc, rms_part, tid), K, rms.eps);
@@ -821,9 +836,12 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
     // lane of a DPP row takes the same branches.
     const int rgrp = tid >> 4, gl = tid & 15;
     const int n_grp = blockDim.x >> 4;
+    // SwiGLU pair: the row sums also go to LDS (over the activation codes,
+    // which no wave reads any more), gate rows first
+    float* srow = reinterpret_cast<float*>(lds);
 #pragma unroll
     for (int cc = 0; cc < C; ++cc) {
-        for (int rl = rgrp; rl < nrows; rl += n_grp) {
+        for (int rl = rgrp; rl < (kSwi ? 2 * nrows : nrows); rl += n_grp) {
             const float* pr = part + cc * rows_per_wg * bpr + rl * bpr;
             float v = 0.0f;
             for (int b = gl; b < bpr; b += 16) v += pr[b];
@@ -831,8 +849,20 @@ __global__ __launch_bounds__(64 * TILE_WAVES) void gemv_tile_kernel(
             v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
             v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
             v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
-            if (gl == 0) Y[cc * ldy_m + (int64_t)(r0 + rl) * ldy_n] = v;
+            if (gl == 0) {
+                if constexpr (kSwi) {
+                    float* const Yp = rl < nrows ? Y : grp.Y[1];
+                    if (Yp) Yp[(int64_t)(r0 + (rl < nrows ? rl : rl - nrows)) * ldy_n] = v;
+                    srow[rl] = v;
+                } else {
+                    Y[cc * ldy_m + (int64_t)(r0 + rl) * ldy_n] = v;
+                }
+            }
         }
+    }
+    if constexpr (kSwi) {
+        __syncthreads();
+        for (int j = tid; j < nrows; j += blockDim.x) rms.S[r0 + j] = swiglu(srow[j], srow[nrows + j]);
     }
 }
 
@@ -1131,7 +1161,8 @@ hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y
 template <int MODE>
 static void launch_rms_tile(dim3 grid, dim3 block, size_t lds, hipStream_t stream, const GemvGroup& grp,
                             const float* X, int64_t K, int64_t R, const RmsArgs& a) {
-    hipLaunchKernelGGL((gemv_tile_kernel<1, 2, false, false, true, MODE>), grid, block, lds, stream, grp, nullptr,
+    // grouped tiles (one matrix per tile), except the SwiGLU pair (bit 6): both matrices per tile
+    hipLaunchKernelGGL((gemv_tile_kernel<1, 2, false, false, (MODE & 64) == 0, MODE>), grid, block, lds, stream, grp, nullptr,
                        nullptr, X, 0, 1, (int)K, 1, (int)R, nullptr, a);
 }
 
@@ -1166,12 +1197,61 @@ hipError_t launch_gemv_rms_group(int count, const uint8_t* const* W, float* cons
     const size_t lds = h_off + (size_t)K * 4;
     if (lds > GEMV_LDS_BUDGET || wgs > 0x7FFFFFFF) return hipErrorNotSupported;
     const dim3 grid((unsigned)wgs), block(64 * TILE_WAVES);
-    const RmsArgs a{R, H, gamma, eps};
+    const RmsArgs a{R, H, gamma, eps, nullptr};
     switch ((R ? 2 : 0) | (gamma ? 4 : 0)) {
         case 0: launch_rms_tile<1>(grid, block, lds, stream, grp, X, K, Rr, a); break;
         case 2: launch_rms_tile<3>(grid, block, lds, stream, grp, X, K, Rr, a); break;
         case 4: launch_rms_tile<5>(grid, block, lds, stream, grp, X, K, Rr, a); break;
         default: launch_rms_tile<7>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+    }
+    return hipGetLastError();
+}
+
+// RMS norm + the gate/up pair of a SwiGLU MLP + the SwiGLU itself, one launch
+// (bs = 1): every workgroup runs the norm's passes as above, then streams the
+// same R rows of gate and of up as one run of steps, and its epilogue writes
+// the rows' gate and up outputs (when Yg / Yu are given) and
+// S = silu(gate) * up with the SwiGLU producer's arithmetic (act_device.h).
+// Rows are computed exactly as by launch_gemv_rms_group on (gate, up), so Yg,
+// Yu and h are those bits, and S is the producer's fp32 value of them.  R
+// divides N, so every tile is whole, with R * K/256 a multiple of 8 (whole
+// steps) and about N / CUs rows (one tile per CU); hipErrorNotSupported when
+// no such R exists, or as launch_gemv_rms_group.
+hipError_t launch_gemv_rms_swiglu(const uint8_t* Wg, const uint8_t* Wu, float* Yg, float* Yu, float* S, int64_t N,
+                                  const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                                  hipStream_t stream) {
+    clear_launch_error();
+    const int64_t bpr = K / QK_K, nb = K / QK8_1;
+    if (bpr < 8 || K > RMS_ONE_BATCH_K || N < 1 || N >= ((int64_t)1 << 30)) return hipErrorNotSupported;
+    const int64_t g = 8 / std::gcd<int64_t, int64_t>(bpr, 8);
+    const int64_t cus = device_cu_count();
+    int64_t Rr = 0;
+    // the epilogue parks 2R row sums over the K bytes of activation codes
+    for (int64_t r = g * (((N + cus - 1) / cus + g - 1) / g); r <= N && 8 * r <= K; r += g) {
+        if (N % r == 0) {
+            Rr = r;
+            break;
+        }
+    }
+    if (Rr == 0 || Rr * bpr * BLOCK_BYTES >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    GemvGroup grp{};
+    for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
+        grp.W[i] = i == 1 ? Wu : Wg;
+        grp.Y[i] = i == 1 ? Yu : Yg;
+        grp.ldy_m[i] = N;
+        grp.N[i] = (int)N;
+        grp.tile_end[i] = (int)(N / Rr);
+    }
+    const size_t h_off = ((size_t)K + (size_t)nb * 4 + (size_t)2 * Rr * bpr * 4 + 15) & ~(size_t)15;
+    const size_t lds = h_off + (size_t)K * 4;
+    if (lds > GEMV_LDS_BUDGET) return hipErrorNotSupported;
+    const dim3 grid((unsigned)(N / Rr)), block(64 * TILE_WAVES);
+    const RmsArgs a{R, H, gamma, eps, S};
+    switch ((R ? 2 : 0) | (gamma ? 4 : 0)) {
+        case 0: launch_rms_tile<1 | 64>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+        case 2: launch_rms_tile<3 | 64>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+        case 4: launch_rms_tile<5 | 64>(grid, block, lds, stream, grp, X, K, Rr, a); break;
+        default: launch_rms_tile<7 | 64>(grid, block, lds, stream, grp, X, K, Rr, a); break;
     }
     return hipGetLastError();
 }

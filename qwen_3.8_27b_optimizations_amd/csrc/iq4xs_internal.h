@@ -67,6 +67,10 @@ hipError_t launch_gemv_fused(const uint8_t* W, const float* X, int64_t sc, int64
 hipError_t launch_gemv_rms_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
                                  const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
                                  hipStream_t stream);
+// RMS norm + gate/up pair + SwiGLU in one bs=1 launch (S = silu(gate) * up).
+hipError_t launch_gemv_rms_swiglu(const uint8_t* Wg, const uint8_t* Wu, float* Yg, float* Yu, float* S, int64_t N,
+                                  const float* X, const float* R, float* H, const float* gamma, float eps, int64_t K,
+                                  hipStream_t stream);
 
 // Same contract on the matrix-core GEMM path (any M >= 1); it also reads the
 // workspace's fp16 code pairs ahq.

@@ -24,6 +24,7 @@
 // rounds as written (division and sqrt are IEEE, the HIP default).
 #include "iq4xs_device.h"
 #include "iq4xs_internal.h"
+#include "act_device.h"
 #include "q8_1_block.h"
 #include "rms_device.h"
 
@@ -31,27 +32,7 @@
 
 namespace iq4xs {
 
-// exp(x) for x <= 88.72283935546875 (+inf above); inputs below -87 are
-// raised to -87 so that no result is subnormal.  ln2 = 0x1.62e4p-1 (16
-// significant bits: n * head is exact) + 0x1.7f7d1cp-20.
-__device__ inline float exp_cody_waite(float x) {
-    if (x > 0x1.62e430p+6f) return __builtin_inff();
-    x = (x < -87.0f) ? -87.0f : x;  // NaN compares false and passes through
-    const float n = __builtin_rintf(x * 0x1.715476p+0f);
-    float r = __builtin_fmaf(-n, 0x1.62e400p-1f, x);
-    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
-    float p = 0x1.a01a02p-13f;  // 1/7!
-    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
-    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
-    p = __builtin_fmaf(p, r, 0.5f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
-}
-
-__device__ inline float silu(float g) { return g / (1.0f + exp_cody_waite(-g)); }
+// exp_cody_waite, silu and swiglu: act_device.h (shared with the GEMV's SwiGLU epilogue).
 
 // One 32-element block by the 8-lane group of lane L: values y at j, j+8,
 // j+16, j+24 (j = q8_lane_elem(L)) -> codes, ds and the fp16 code pairs
@@ -78,8 +59,7 @@ __global__ __launch_bounds__(256) void swiglu_q8_1_kernel(const float* __restric
     float y[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float s = silu(G[e + 8 * i]);
-        y[i] = s * U[e + 8 * i];
+        y[i] = swiglu(G[e + 8 * i], U[e + 8 * i]);
     }
     store_block8(quantize_block8(y[0], y[1], y[2], y[3]), qs + e, ds + blk, hq + blk * 16, j);
 }

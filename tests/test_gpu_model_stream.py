@@ -2,12 +2,14 @@
 12.30 GB of IQ4_XS resident): bench.py's own chain (bench.ModelChain) on the
 GPU, checked against the oracle.
 
-* Two layers through every variant -- plain, grouped and rms-fused at bs=1,
-  plain and grouped at M=512 -- at the full config-1 shapes: every producer's
-  Q8_1 blocks (and the residual stream h) bit for bit against the oracle's
-  rms norm / swiglu; every projection on sampled rows within rel-L2 1e-4 of
-  the reference GEMM semantics on the blocks it read.
-* The full 64-layer bs=1 chain: finite, the three variants bit-identical to
+* Two layers through every variant -- plain, grouped, rms-fused and
+  rms+swiglu-fused at bs=1, plain and grouped at M=512 -- at the full
+  config-1 shapes: every producer's Q8_1 blocks (and the residual stream h)
+  bit for bit against the oracle's rms norm / swiglu, the fused SwiGLU's fp32
+  silu(gate) * up bit for bit against the oracle's; every projection on
+  sampled rows within rel-L2 1e-4 of the reference GEMM semantics on the
+  blocks it read.
+* The full 64-layer bs=1 chain: finite, the four variants bit-identical to
   each other, and a replay bit-identical to the first run.
 """
 import numpy as np
@@ -107,26 +109,36 @@ class Checker:
             assert np.array_equal(self.blocks(t["ws"], FF_DIM), Q), (l, "swiglu", "Q8_1")
         elif stage == "down":
             self.proj(l, stage, "down_proj", self.blocks(t["ws"], FF_DIM), t["down"])
+        elif stage == "rms_gate_up_swiglu":
+            Q = self.rms(l, stage, t["h_in"], t["r_in"], t["h_out"])
+            for name, key in (("gate_proj", "gate"), ("up_proj", "up")):
+                self.proj(l, stage, name, Q, t[key])
+            g, u = t["gate"].cpu().numpy().ravel(), t["up"].cpu().numpy().ravel()
+            S_ref = (self.orc.silu(g) * u).astype(np.float32)
+            assert np.array_equal(bits(t["s"]).ravel(), S_ref.view(np.uint32)), (l, stage, "S")
+        elif stage == "down_from_s":
+            AQ = self.orc.quantize_q8_1_batched(t["x"].cpu().numpy(), FF_DIM, self.M, LAYOUT_MK)
+            self.proj(l, stage, "down_proj", AQ, t["down"])
         else:
             raise AssertionError(stage)
 
 
-@pytest.mark.parametrize("M,variant", [(1, "plain"), (1, "grouped"), (1, "fused"), (512, "plain"),
-                                       (512, "grouped")])
+@pytest.mark.parametrize("M,variant", [(1, "plain"), (1, "grouped"), (1, "fused"), (1, "fused_swiglu"),
+                                       (512, "plain"), (512, "grouped")])
 def test_two_layers_against_oracle(pkg, orc, bench, model, dev, M, variant):
     print(f"[model-stream] two checked layers M={M} variant={variant}", flush=True)
     chain = bench.ModelChain(torch, pkg, pkg.lib(), model, M, torch.cuda.current_stream(), variant)
     chk = Checker(pkg, orc, bench, model, M)
     chain.run(2, check=chk)
     assert chain.finite()
-    per_layer = 5 if variant == "fused" else 7
+    per_layer = {"fused": 5, "fused_swiglu": 4}.get(variant, 7)
     assert len(chk.seen) == 2 * per_layer
 
 
 def test_64_layers_bs1_variants_bit_identical(pkg, bench, model, dev):
     stream = torch.cuda.current_stream()
     states = {}
-    for variant in ("plain", "grouped", "fused", "plain"):
+    for variant in ("plain", "grouped", "fused", "fused_swiglu", "plain"):
         print(f"[model-stream] 64 layers bs=1 variant={variant}", flush=True)
         chain = bench.ModelChain(torch, pkg, pkg.lib(), model, 1, stream, variant)
         chain.run()
@@ -136,7 +148,7 @@ def test_64_layers_bs1_variants_bit_identical(pkg, bench, model, dev):
             assert all(np.array_equal(a, b) for a, b in zip(states[variant], snap)), "replay differs"
         states[variant] = snap
         del chain
-    for variant in ("grouped", "fused"):
+    for variant in ("grouped", "fused", "fused_swiglu"):
         for j, (a, b) in enumerate(zip(states["plain"], states[variant])):
             assert np.array_equal(a, b), (variant, j)
     # the chain did run: the last layer's outputs are not the initial zeros
