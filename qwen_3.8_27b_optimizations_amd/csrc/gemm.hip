@@ -498,6 +498,15 @@ constexpr int H_T_OFF = H_BM * H_ROW;                // token scale pairs, uint3
 constexpr int H_T_COPY = H_BM * 8 * 4;               // copy h of them feeds lane half h
 constexpr int H_STAGE = H_T_OFF + 2 * H_T_COPY;      // 72 KB
 constexpr int H_LUT = 1024;                          // the code pair table
+// The same stage layout for a tile of at most TOK tokens: half-height tiles
+// (64 rows, 4 waves, at most 64 tokens) use TOK = 64, so that two of them
+// fit a CU's LDS.
+template <int TOK>
+struct HStage {
+    static constexpr int t_off = TOK * H_ROW;
+    static constexpr int t_copy = TOK * 8 * 4;
+    static constexpr int bytes = t_off + 2 * t_copy;
+};
 // the table and two stages: 145 KB of gfx950's 160 KB of LDS per CU
 
 __device__ inline int h_chunk(int m, int c) { return m * H_ROW + ((c ^ (m & 15)) << 4); }
@@ -587,7 +596,7 @@ struct HWeights {  // one super-block of this lane's weight row: header, and qs 
 // flight; the next sub-block's weights are decoded during the current one.
 // `w` is reloaded with the next super-block (load_next) once its last
 // sub-block is decoded, so one set of weight registers serves both.
-template <bool kDebug, int T, typename LoadNext>
+template <bool kDebug, int T, int TOK, typename LoadNext>
 __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t* lut, HWeights& w, v16f (&acc)[4],
                                                int kh, int h, int col, int lane, int64_t kb, int64_t m0, int64_t M,
                                                int64_t n, int64_t N, int64_t nb, int32_t* __restrict__ dbg,
@@ -632,7 +641,7 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
         if (r < 2)
             a = *reinterpret_cast<const v4u*>(st + h_chunk(m, 4 * s + 2 * h + r));
         else
-            a = *reinterpret_cast<const v4u*>(st + H_T_OFF + h * H_T_COPY + m * 32 + 16 * kh);
+            a = *reinterpret_cast<const v4u*>(st + HStage<TOK>::t_off + h * HStage<TOK>::t_copy + m * 32 + 16 * kh);
     };
     // half q of the epilogue of step t: acc += sp * dp for accumulators 8q .. 8q + 7
     auto epilogue = [&](int t, const v16f& dp, const v16f& sp, int q) {
@@ -707,16 +716,23 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
 // One 128-row x 32T-token tile (T token blocks per wave; the per-output
 // arithmetic does not depend on T, so neither do the results).
 // W, Y, N, ldy_m: the tile's matrix, whose first row tile is tile0.
-template <bool kDebug, int T>
+// RG row groups of 32 rows (4: the 128-row tile of 8 waves; 2: the 64-row
+// half-height tile of 4 waves, at most 64 tokens); wave w computes row group
+// w % RG on the sub-block half w / RG, so a row's arithmetic is the same in
+// both.
+template <bool kDebug, int T, int RG>
 __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* __restrict__ Y, int64_t N,
                                          int64_t ldy_m, int tile0, const uint32_t* __restrict__ ahq,
                                          const uint32_t* __restrict__ ads, int64_t K, int64_t M, int64_t ldy_n, int bx,
                                          int by, uint8_t* smem, int32_t* __restrict__ dbg) {
-    uint8_t(*const stages)[H_STAGE] = reinterpret_cast<uint8_t(*)[H_STAGE]>(smem + H_LUT);
+    static_assert(RG == 4 || (RG == 2 && T <= 2), "half-height tiles hold at most 64 tokens");
+    constexpr int TOK = 32 * RG, STAGE = HStage<TOK>::bytes;
+    constexpr int CPW = 8 * T / RG;  // 1 KB token copies per wave and stage (16 T per stage)
+    uint8_t(*const stages)[STAGE] = reinterpret_cast<uint8_t(*)[STAGE]>(smem + H_LUT);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
-    const int rg = wave & 3, kh = wave >> 2, h = lane >> 5, col = lane & 31;
-    const int64_t n0 = (int64_t)(bx - tile0) * H_BN;
+    const int rg = wave % RG, kh = wave / RG, h = lane >> 5, col = lane & 31;
+    const int64_t n0 = (int64_t)(bx - tile0) * (32 * RG);
     const int64_t m0 = (int64_t)by * (32 * T);
     const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
 
@@ -732,22 +748,22 @@ __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* _
     };
 
     // ---- token staging (32 T token rows of 512 bytes): instruction i of this
-    // wave fills LDS chunks (wave * 2T + i) * 64 + lane of a stage, i.e. row
-    // 4T wave + 2i + h, chunk col ^ (row & 15) of it (the swizzle)
+    // wave fills LDS chunks (wave * CPW + i) * 64 + lane of a stage, i.e. row
+    // 2 CPW wave + 2i + h, chunk col ^ (row & 15) of it (the swizzle)
     const uint8_t* xtile = reinterpret_cast<const uint8_t*>(ahq) + m0 * (2 * K);
-    const int xrow = 4 * T * wave + h, xlast = (int)min<int64_t>(M - 1 - m0, 32 * T - 1);  // rows past M repeat the last
+    const int xrow = 2 * CPW * wave + h, xlast = (int)min<int64_t>(M - 1 - m0, 32 * T - 1);  // rows past M repeat the last
     const uint32_t xstride = (uint32_t)(2 * K);
-    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_addr(&stages[0][0]) + wave * 2 * T * 1024);
-    // for T != 3 the bits of xrow & 15 and of 2i are disjoint, so the
+    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_addr(&stages[0][0]) + wave * CPW * 1024);
+    // for CPW = 2, 4, 8 the bits of xrow & 15 and of 2i are disjoint, so the
     // swizzled chunk is (col ^ (xrow & 15)) ^ 2i: one XOR per copy
     const uint32_t xcol = 16u * (uint32_t)(col ^ (xrow & 15));
     auto issue_x = [&](int64_t kb, int stage) {
         const uint8_t* src = xtile + kb * 512;
 #pragma unroll
-        for (int i = 0; i < 2 * T; ++i) {
+        for (int i = 0; i < CPW; ++i) {
             const int m = xrow + 2 * i;
-            const uint32_t c16 = T == 3 ? 16u * (uint32_t)(col ^ (m & 15)) : (xcol ^ (32u * i));
-            dma16(src, (uint32_t)min(m, xlast) * xstride + c16, lds_wave + stage * H_STAGE + i * 1024);
+            const uint32_t c16 = (CPW & (CPW - 1)) ? 16u * (uint32_t)(col ^ (m & 15)) : (xcol ^ (32u * i));
+            dma16(src, (uint32_t)min(m, xlast) * xstride + c16, lds_wave + stage * STAGE + i * 1024);
         }
     };
     // token scales: thread tid -> token tid >> 2, sub-blocks 2 (tid & 3), + 1
@@ -758,11 +774,11 @@ __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* _
     // copy 1 (lane half 1, which meets the weight scale's low half) has 0
     // for a non-finite d_x, so that no Inf meets a zero low half (0 * Inf)
     auto store_d = [&](v2u d, uint8_t* stage) {
-        uint32_t* t = reinterpret_cast<uint32_t*>(stage + H_T_OFF) + tm * 8 + ts;
+        uint32_t* t = reinterpret_cast<uint32_t*>(stage + HStage<TOK>::t_off) + tm * 8 + ts;
         const float x0 = half_bits_to_float(d.x & 0xFFFFu), x1 = half_bits_to_float(d.y & 0xFFFFu);
         const v2u p = v2u{bf16_pair_f(x0), bf16_pair_f(x1)};
         *reinterpret_cast<v2u*>(t) = p;
-        *reinterpret_cast<v2u*>(t + H_T_COPY / 4) =
+        *reinterpret_cast<v2u*>(t + HStage<TOK>::t_copy / 4) =
             v2u{__builtin_isfinite(x0) ? p.x : 0u, __builtin_isfinite(x1) ? p.y : 0u};
     };
 
@@ -797,7 +813,7 @@ __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* _
         const int64_t kb1 = min(kb + 1, bpr - 1), kb2 = min(kb + 2, bpr - 1);
         issue_x(kb1, cur ^ 1);
         v2u dnext = load_d(kb1);
-        f16_superblock<kDebug, T>(stages[cur], smem, wc, acc, kh, h, col, lane, kb, m0, M, n, N, nb, dbg,
+        f16_superblock<kDebug, T, TOK>(stages[cur], smem, wc, acc, kh, h, col, lane, kb, m0, M, n, N, nb, dbg,
                                [&](HWeights& g) { load_w(g, kb2); });
         // this thread's direct-to-LDS copies and token scales have landed; the
         // 5 weight loads of super-block kb + 2, issued after them, may still
@@ -871,13 +887,16 @@ struct F16Plan {
     F16Seg seg[F16_SEGS];
 };
 
-template <bool kDebug, bool kGroup>
-__global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp, const uint32_t* __restrict__ ahq,
-                                                             const uint32_t* __restrict__ ads, int64_t K, int64_t M,
-                                                             int64_t ldy_n, const F16Plan plan,
-                                                             int32_t* __restrict__ dbg) {
+// RG = 4: 128-row tiles of 8 waves (one workgroup per CU); RG = 2: 64-row
+// tiles of 4 waves and at most 64 tokens (two per CU), for launches with too
+// few big tiles to fill the CUs.  A row's arithmetic is the same in both.
+template <bool kDebug, bool kGroup, int RG = 4>
+__global__ __launch_bounds__(128 * RG) void gemm_f16_kernel(const GemmGroup grp, const uint32_t* __restrict__ ahq,
+                                                            const uint32_t* __restrict__ ads, int64_t K, int64_t M,
+                                                            int64_t ldy_n, const F16Plan plan,
+                                                            int32_t* __restrict__ dbg) {
     // LDS: the 1 KB code pair table at address 0, then the two stages
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[H_LUT + 2 * H_STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[H_LUT + 2 * HStage<32 * RG>::bytes];
     const int b = (int)blockIdx.x;
     // the segment (scalar selects on the by-value plan)
     int g = 0;
@@ -921,11 +940,16 @@ __global__ __launch_bounds__(H_THREADS) void gemm_f16_kernel(const GemmGroup grp
             }
         }
     }
-    switch (sg.T) {
-        case 1: f16_tile<kDebug, 1>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
-        case 2: f16_tile<kDebug, 2>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
-        case 3: f16_tile<kDebug, 3>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
-        default: f16_tile<kDebug, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+    if constexpr (RG == 2) {
+        if (sg.T == 1) f16_tile<kDebug, 1, 2>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg);
+        else f16_tile<kDebug, 2, 2>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg);
+    } else {
+        switch (sg.T) {
+            case 1: f16_tile<kDebug, 1, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+            case 2: f16_tile<kDebug, 2, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+            case 3: f16_tile<kDebug, 3, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+            default: f16_tile<kDebug, 4, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+        }
     }
 }
 
@@ -1050,6 +1074,22 @@ template <bool kDebug, bool kGroup>
 static hipError_t launch_f16_kernel(const GemmGroup& grp, int64_t row_tiles, const uint32_t* ahq, const uint32_t* ads,
                                     int64_t K, int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     if (row_tiles * f16_token_tiles(M, 1) > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    // Half-height tiles (64 rows, 4 waves, one token block each) when even
+    // single-block 128-row tiles would fill at most half the CUs (k/v at
+    // M = 512: 128 -> 256 workgroups, 37 -> 33 us).  They run slower per
+    // row than big tiles wherever those fill the chip, so only there.
+    const int64_t cus = device_cu_count();
+    if (!kGroup && !kDebug && row_tiles * f16_token_tiles(M, 1) * 2 <= cus) {
+        GemmGroup g2 = grp;
+        const int64_t rt2 = (grp.N[0] + 63) / 64;
+        g2.tile_end[0] = (int)rt2;
+        const F16Plan plan = f16_plan_of({{rt2, 1}}, M);
+        const int wgs = plan.seg[F16_SEGS - 1].wg_end;
+        if (wgs <= 0) return hipSuccess;
+        hipLaunchKernelGGL((gemm_f16_kernel<false, false, 2>), dim3((unsigned)wgs), dim3(256), 0, stream, g2, ahq,
+                           ads, K, M, ldy_n, plan, dbg);
+        return hipGetLastError();
+    }
     const F16Plan plan = kDebug ? f16_plan_of({{row_tiles, 4}}, M) : f16_plan(row_tiles, M);
     const int wgs = plan.seg[F16_SEGS - 1].wg_end;
     if (wgs <= 0) return hipSuccess;
