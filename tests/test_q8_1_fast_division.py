@@ -1,8 +1,9 @@
 """CPU check of the argument behind the Q8_1 quantiser's division shortcut
-(csrc/q8_1_block.h, round_div): with r = 1/d from a reciprocal instruction
+(csrc/q8_1_block.h, round_codes): with r = 1/d from a reciprocal instruction
 that is within 1 ulp, p = x*r rounds to the same integer as roundf(x/d)
-whenever |frac(|p|) - 1/2| >= 2^-14; every other lane takes the exact
-division.  Emulated here in numpy with r perturbed by -1, 0 and +1 ulp and
+whenever |frac(|p|) - 1/2| >= 2^-14; a lane holding any other value
+recomputes its values by the exact division (which is right for all of
+them).  Emulated here in numpy with r perturbed by -1, 0 and +1 ulp and
 compared with the oracle's codes, on blocks built to sit on and near the
 rounding boundaries and on ordinary activations."""
 import numpy as np
