@@ -482,17 +482,18 @@ def main() -> int:
 
     groups = [(group_args(layers[l][0:3], ys[0:3]), group_args(layers[l][4:6], ys[4:6])) for l in range(args.layers)]
 
-    def grouped_rotation() -> None:
+    def grouped_rotation(wsb, yb, M, grp) -> None:
         for l in range(args.layers):
-            (n, wp, yp, nn), (n2, wp2, yp2, nn2) = groups[l]
-            L.check("iq4xs_mul_mat_q8_1_group", n, wp, yp, nn, wss[0].data_ptr(), SHAPES[0][1], 1, pkg.LAYOUT_MK, s)
-            L.check("iq4xs_mul_mat_q8_1", layers[l][3].data_ptr(), wss[3].data_ptr(), ys[3].data_ptr(), SHAPES[3][1],
-                    SHAPES[3][2], 1, pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
-            L.check("iq4xs_mul_mat_q8_1_group", n2, wp2, yp2, nn2, wss[4].data_ptr(), SHAPES[4][1], 1, pkg.LAYOUT_MK, s)
-            L.check("iq4xs_mul_mat_q8_1", layers[l][6].data_ptr(), wss[6].data_ptr(), ys[6].data_ptr(), SHAPES[6][1],
-                    SHAPES[6][2], 1, pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
+            (n, wp, yp, nn), (n2, wp2, yp2, nn2) = grp[l]
+            L.check("iq4xs_mul_mat_q8_1_group", n, wp, yp, nn, wsb[0].data_ptr(), SHAPES[0][1], M, pkg.LAYOUT_MK, s)
+            L.check("iq4xs_mul_mat_q8_1", layers[l][3].data_ptr(), wsb[3].data_ptr(), yb[3].data_ptr(), SHAPES[3][1],
+                    SHAPES[3][2], M, pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
+            L.check("iq4xs_mul_mat_q8_1_group", n2, wp2, yp2, nn2, wsb[4].data_ptr(), SHAPES[4][1], M, pkg.LAYOUT_MK,
+                    s)
+            L.check("iq4xs_mul_mat_q8_1", layers[l][6].data_ptr(), wsb[6].data_ptr(), yb[6].data_ptr(), SHAPES[6][1],
+                    SHAPES[6][2], M, pkg.LAYOUT_MK, pkg.PATH_GEMV, s)
 
-    gr_run, _ = capture(torch, stream, grouped_rotation, use_graph)
+    gr_run, _ = capture(torch, stream, lambda: grouped_rotation(wss, ys, 1, groups), use_graph)
     timer(gr_run, 2)
     gr_us = timer(gr_run, args.roofline_reps) / args.roofline_reps
     gr_gbs = step_bytes * args.layers / (gr_us * 1e-6) / 1e9
@@ -568,7 +569,18 @@ def main() -> int:
         small[str(M)] = {"GBps": round(b_bytes / (us * 1e-6) / 1e9, 1),
                          "frac": round(b_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                          "us_per_layer": round(us / args.layers, 2)}
-        del X, wsb, yb, brun
+        # the same rotation with q,k,v and gate,up each one grouped launch
+        # (matrix-core matrices of one wave count share a launch)
+        # group_args reads N from the outputs' element count: M rows of N
+        bgroups = [(group_args(layers[l][0:3], [y[0] for y in yb[0:3]]),
+                    group_args(layers[l][4:6], [y[0] for y in yb[4:6]])) for l in range(args.layers)]
+        bgrun, _ = capture(torch, stream, lambda: grouped_rotation(wsb, yb, M, bgroups), use_graph)
+        timer(bgrun, 2)
+        gus = timer(bgrun, max(4, args.roofline_reps // 4)) / max(4, args.roofline_reps // 4)
+        small[str(M)]["grouped"] = {"GBps": round(b_bytes / (gus * 1e-6) / 1e9, 1),
+                                    "frac": round(b_bytes / (gus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                    "us_per_layer": round(gus / args.layers, 2)}
+        del X, wsb, yb, brun, bgrun, bgroups
 
     # ---- IQ4_XS -> fp32 dequantiser (136 B in, 1024 B out per super-block) --
     dq_bytes, dq_us = 0, 0.0

@@ -1133,26 +1133,59 @@ hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y
     for (int i = 0; i < count; ++i) mats[i] = {W[i], Y[i], N[i], layout_mk ? N[i] : 1};
     const int64_t ldy_n = layout_mk ? 1 : M;
     static const int kind = tuning_knob("IQ4XS_GEMV_KIND", 2, 0, 2);
+    // matrix-core matrices first, one launch per wave count (the same
+    // routing and kernel as single calls)
+    TileMat rest[GEMV_GROUP_MAX];
+    int n_rest = 0;
+    bool done[GEMV_GROUP_MAX] = {};
+    for (int i = 0; i < count; ++i) {
+        if (done[i]) continue;
+        if (!use_gemv_mfma(N[i], M)) {
+            rest[n_rest++] = mats[i];
+            continue;
+        }
+        const uint8_t* gW[GEMV_GROUP_MAX];
+        float* gY[GEMV_GROUP_MAX];
+        int64_t gN[GEMV_GROUP_MAX], gL[GEMV_GROUP_MAX];
+        int n = 0;
+        const int waves = gemv_mfma_waves(N[i]);
+        for (int j = i; j < count; ++j) {
+            if (done[j] || !use_gemv_mfma(N[j], M) || gemv_mfma_waves(N[j]) != waves) continue;
+            gW[n] = W[j];
+            gY[n] = Y[j];
+            gN[n] = N[j];
+            gL[n] = mats[j].ldy_m;
+            ++n;
+            done[j] = true;
+        }
+        hipError_t err = launch_gemv_mfma_group(n, gW, gY, gN, gL, aqs, ads, K, M, ldy_n, nullptr, stream);
+        if (err == hipErrorNotSupported) {  // shapes past its offsets take the single-call route
+            err = hipSuccess;
+            for (int j = 0; j < n && err == hipSuccess; ++j)
+                err = dispatch_cols(gW[j], aqs, ads, nullptr, 0, 0, gY[j], K, gN[j], M, gL[j], ldy_n, nullptr, stream);
+        }
+        if (err != hipSuccess) return err;
+    }
+    if (n_rest == 0) return hipSuccess;
     hipError_t err = hipErrorNotSupported;
-    bool any_mfma = false;
-    for (int i = 0; i < count; ++i) any_mfma = any_mfma || use_gemv_mfma(N[i], M);
-    if (K / QK_K >= 8 && K <= (1 << 24) && kind == 2 && !any_mfma) {
+    if (K / QK_K >= 8 && K <= (1 << 24) && kind == 2) {
         switch (M) {
-            case 1: err = launch_tile_group<1>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
-            case 2: err = launch_tile_group<2>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
-            case 3: err = launch_tile_group<3>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
-            case 4: err = launch_tile_group<4>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
-            case 5: err = launch_tile_group<5>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
-            case 6: err = launch_tile_group<6>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
-            case 7: err = launch_tile_group<7>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
-            case 8: err = launch_tile_group<8>(mats, count, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 1: err = launch_tile_group<1>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 2: err = launch_tile_group<2>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 3: err = launch_tile_group<3>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 4: err = launch_tile_group<4>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 5: err = launch_tile_group<5>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 6: err = launch_tile_group<6>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 7: err = launch_tile_group<7>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
+            case 8: err = launch_tile_group<8>(rest, n_rest, aqs, ads, nullptr, 0, 0, K, ldy_n, nullptr, stream); break;
             default: return hipErrorInvalidValue;
         }
         if (err != hipErrorNotSupported) return err;
     }
     // shapes the tile kernel does not take: one launch per matrix
-    for (int i = 0; i < count; ++i) {
-        err = dispatch_cols(W[i], aqs, ads, nullptr, 0, 0, Y[i], K, N[i], M, mats[i].ldy_m, ldy_n, nullptr, stream);
+    for (int i = 0; i < n_rest; ++i) {
+        err = dispatch_cols(rest[i].W, aqs, ads, nullptr, 0, 0, rest[i].Y, K, rest[i].N, M, rest[i].ldy_m, ldy_n,
+                            nullptr, stream);
         if (err != hipSuccess) return err;
     }
     return hipSuccess;

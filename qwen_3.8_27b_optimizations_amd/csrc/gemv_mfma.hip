@@ -61,15 +61,43 @@ struct GmA {      // activations of one super-block (L2-resident: one ahead)
     uint32_t ds; // Q8_1 ds word of token lane/8, sub-block lane%8
 };
 
+// The matrices of one launch (same K and activations): workgroups
+// [tile_end[i-1], tile_end[i]) run matrix i, rows[i] rows each.  Entries past
+// the group's count repeat its last matrix with tile_end = the grid size, so
+// no workgroup selects them.
+struct GmGroup {
+    const uint8_t* W[GEMV_GROUP_MAX];
+    float* Y[GEMV_GROUP_MAX];
+    int64_t ldy_m[GEMV_GROUP_MAX];
+    int N[GEMV_GROUP_MAX];
+    int rows[GEMV_GROUP_MAX];
+    int tile_end[GEMV_GROUP_MAX];
+};
+
 template <int GM_WAVES, bool kDebug>
-__global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t* __restrict__ W,
+__global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const GmGroup grp,
                                                                   const int8_t* __restrict__ aqs,
-                                                                  const uint32_t* __restrict__ ads,
-                                                                  float* __restrict__ Y, int K, int N, int M,
-                                                                  int rows, int64_t ldy_m, int64_t ldy_n,
-                                                                  int32_t* __restrict__ dbg) {
+                                                                  const uint32_t* __restrict__ ads, int K, int M,
+                                                                  int64_t ldy_n, int32_t* __restrict__ dbg) {
     constexpr int G = 1;  // M <= 8: tokens 4h + e of element e < 4
     extern __shared__ __attribute__((aligned(16))) float gm_lds[];
+    // this workgroup's matrix: scalar selects on the by-value descriptor (a
+    // dynamic index into it would go through scratch)
+    const uint8_t* __restrict__ W = grp.W[0];
+    float* __restrict__ Y = grp.Y[0];
+    int64_t ldy_m = grp.ldy_m[0];
+    int N = grp.N[0], rows = grp.rows[0], tile0 = 0;
+#pragma unroll
+    for (int i = 1; i < GEMV_GROUP_MAX; ++i) {
+        if ((int)blockIdx.x >= grp.tile_end[i - 1]) {
+            W = grp.W[i];
+            Y = grp.Y[i];
+            ldy_m = grp.ldy_m[i];
+            N = grp.N[i];
+            rows = grp.rows[i];
+            tile0 = grp.tile_end[i - 1];
+        }
+    }
     const int bpr = K / QK_K, nb = K / QK8_1;
     float* red = gm_lds;                        // [GM_WAVES][4G][64] partial sums
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, col = lane & 31;
@@ -77,7 +105,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     uint8_t* sw = swave;                                          // [32][144] qs of the 32 rows
     int8_t* sact = reinterpret_cast<int8_t*>(swave + 32 * GM_WROW);  // [8][272] activations
     const int wave = tid >> 6;
-    const int r0 = blockIdx.x * rows;
+    const int r0 = ((int)blockIdx.x - tile0) * rows;
     const int nrow = min(rows, N - r0);  // this workgroup's rows (1..32; MFMA rows past them are masked)
     // Global loads are 32-bit lane offsets from workgroup-uniform bases (a
     // 32-row block spans 32 * K/256 * 136 bytes), which keeps the load ring
@@ -195,14 +223,42 @@ __global__ __launch_bounds__(64 * GM_WAVES) void gemv_mfma_kernel(const uint8_t*
     }
 }
 
+// Workgroups and rows per workgroup of one matrix.  The wave count fixes each
+// row's fp32 summation order; the rows per workgroup only balance the grid (a
+// row's arithmetic does not depend on them).
+struct GmPlan {
+    int waves, rows;
+};
+
+static GmPlan gm_plan(int64_t N) {
+    // Parallelism comes from splitting K over the waves of a row block: with
+    // fewer 32-row blocks than two per CU, 16 waves each (measured: q, o and
+    // down 5-15 % faster), otherwise 8 (gate/up: 16 would leave fewer
+    // workgroups resident per CU).  With 16 waves the rows per workgroup (at
+    // most 32, the MFMA's) are chosen so that every CU gets the same number
+    // of workgroups: N = 5120 takes 20 rows on 256 CUs instead of 160 blocks
+    // of 32 that leave 96 CUs idle (bs = 8: down 21.3 -> 18.4-19.5 us, o
+    // unchanged).  Each workgroup decodes all 32 MFMA rows whatever it keeps,
+    // so the 8-wave shapes stay at 32 rows (gate with 17-row workgroups, 4
+    // per CU instead of 2.125: 18.9 -> 21.5 us).
+    //
+    // The wave count is chosen from the shape alone, against MI355X's 256
+    // CUs, so a device or partition with another CU count gives the same
+    // bits; the rows per workgroup use the device's own CU count.
+    constexpr int64_t kWaveChoiceCus = 256;
+    const int64_t cus = device_cu_count();
+    if ((N + 31) / 32 < 2 * kWaveChoiceCus) {
+        const int64_t k = (N + 32 * cus - 1) / (32 * cus);
+        return {16, (int)((N + cus * k - 1) / (cus * k))};
+    }
+    return {8, 32};
+}
+
 template <int WAVES>
-static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K, int64_t N,
-                            int64_t M, int rows, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+static hipError_t launch_gm(const GmGroup& grp, int64_t wgs, const int8_t* aqs, const uint32_t* ads, int64_t K,
+                            int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     const size_t lds = (size_t)WAVES * 4 * 64 * sizeof(float) + (size_t)WAVES * GM_WAVE_LDS;
     if (lds > GM_LDS_MAX) return hipErrorNotSupported;
-    // the kernel's 32-bit load offsets span one 32-row block and 8 token rows
-    if ((int64_t)32 * (K / QK_K) * BLOCK_BYTES >= ((int64_t)1 << 31) || (int64_t)8 * K >= ((int64_t)1 << 31))
-        return hipErrorNotSupported;
     if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit of a launch
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_mfma_kernel<WAVES, false>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS_MAX);
@@ -211,46 +267,52 @@ static hipError_t launch_gm(const uint8_t* W, const int8_t* aqs, const uint32_t*
                                     hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS_MAX);
         if (e != hipSuccess) return e;
     }
-    if (rows < 1 || rows > 32) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((N + rows - 1) / rows)), block(64 * WAVES);
+    const dim3 grid((unsigned)wgs), block(64 * WAVES);
     if (dbg)
-        hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, true>), grid, block, lds, stream, W, aqs, ads, Y, (int)K, (int)N,
-                           (int)M, rows, ldy_m, ldy_n, dbg);
+        hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, true>), grid, block, lds, stream, grp, aqs, ads, (int)K, (int)M,
+                           ldy_n, dbg);
     else
-        hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, false>), grid, block, lds, stream, W, aqs, ads, Y, (int)K,
-                           (int)N, (int)M, rows, ldy_m, ldy_n, dbg);
+        hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, false>), grid, block, lds, stream, grp, aqs, ads, (int)K, (int)M,
+                           ldy_n, dbg);
     return hipGetLastError();
 }
 
+hipError_t launch_gemv_mfma_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
+                                  const int64_t* ldy_m, const int8_t* aqs, const uint32_t* ads, int64_t K,
+                                  int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
+    clear_launch_error();
+    if (count < 1 || count > GEMV_GROUP_MAX || (dbg && count != 1)) return hipErrorInvalidValue;
+    if (M < 1 || M > 8 || K % QK_K || K >= (1 << 24)) return hipErrorNotSupported;
+    // the kernel's 32-bit load offsets span one 32-row block and 8 token rows
+    if ((int64_t)32 * (K / QK_K) * BLOCK_BYTES >= ((int64_t)1 << 31) || (int64_t)8 * K >= ((int64_t)1 << 31))
+        return hipErrorNotSupported;
+    GmGroup grp{};
+    int64_t wgs = 0;
+    int waves = 0;
+    for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
+        const int j = i < count ? i : count - 1;
+        if (N[j] < 1 || N[j] >= (1 << 30)) return hipErrorNotSupported;
+        const GmPlan plan = gm_plan(N[j]);
+        if (i == 0) waves = plan.waves;
+        if (plan.waves != waves) return hipErrorNotSupported;  // one wave count per launch
+        if (i < count) wgs += (N[j] + plan.rows - 1) / plan.rows;
+        if (wgs > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        grp.W[i] = W[j];
+        grp.Y[i] = Y[j];
+        grp.ldy_m[i] = ldy_m[j];
+        grp.N[i] = (int)N[j];
+        grp.rows[i] = plan.rows;
+        grp.tile_end[i] = (int)wgs;
+    }
+    return waves == 16 ? launch_gm<16>(grp, wgs, aqs, ads, K, M, ldy_n, dbg, stream)
+                       : launch_gm<8>(grp, wgs, aqs, ads, K, M, ldy_n, dbg, stream);
+}
+
+int gemv_mfma_waves(int64_t N) { return gm_plan(N).waves; }
+
 hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, float* Y, int64_t K,
                             int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
-    clear_launch_error();
-    if (M < 1 || M > 8 || K % QK_K || K >= (1 << 24) || N >= (1 << 30)) return hipErrorNotSupported;
-    // Parallelism comes from splitting K over the waves of a row block: with
-    // fewer 32-row blocks than two per CU, 16 waves each (measured: q, o and
-    // down 5-15 % faster), otherwise 8 (gate/up: 16 would leave fewer
-    // workgroups resident per CU).  A row's arithmetic depends only on that
-    // wave count.  With 16 waves the rows per workgroup (at most 32, the
-    // MFMA's) are chosen so that every CU gets the same number of workgroups:
-    // N = 5120 takes 20 rows on 256 CUs instead of 160 blocks of 32 that
-    // leave 96 CUs idle (bs = 8: down 21.3 -> 18.4-19.5 us, o unchanged).
-    // Each workgroup decodes all 32 MFMA rows whatever it keeps, so the
-    // 8-wave shapes stay at 32 rows (gate with 17-row workgroups, 4 per CU
-    // instead of 2.125: 18.9 -> 21.5 us).
-    //
-    // The wave count fixes each row's fp32 summation order, so it is chosen
-    // from the shape alone, against MI355X's 256 CUs: a device or partition
-    // with another CU count gives the same bits.  The rows per workgroup only
-    // balance the grid (a row's arithmetic does not depend on them) and use
-    // the device's own CU count.
-    constexpr int64_t kWaveChoiceCus = 256;
-    const int64_t cus = device_cu_count();
-    if ((N + 31) / 32 < 2 * kWaveChoiceCus) {
-        const int64_t k = (N + 32 * cus - 1) / (32 * cus);
-        const int rows = (int)((N + cus * k - 1) / (cus * k));
-        return launch_gm<16>(W, aqs, ads, Y, K, N, M, rows, ldy_m, ldy_n, dbg, stream);
-    }
-    return launch_gm<8>(W, aqs, ads, Y, K, N, M, 32, ldy_m, ldy_n, dbg, stream);
+    return launch_gemv_mfma_group(1, &W, &Y, &N, &ldy_m, aqs, ads, K, M, ldy_n, dbg, stream);
 }
 
 }  // namespace iq4xs

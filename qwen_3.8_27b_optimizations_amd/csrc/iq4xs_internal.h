@@ -47,10 +47,23 @@ hipError_t launch_gemv_mfma(const uint8_t* W, const int8_t* aqs, const uint32_t*
 // Matrices run together by one grouped GEMV launch (same K, same activations).
 constexpr int GEMV_GROUP_MAX = 4;
 
+// The matrix-core GEMV over count <= GEMV_GROUP_MAX matrices in one launch
+// (Y[i] element (m, n) at Y[i][m*ldy_m[i] + n*ldy_n]); every matrix must take
+// the same wave count (gemv_mfma_waves), else hipErrorNotSupported.  dbg only
+// with count == 1.  Outputs are bit-identical to one launch per matrix.
+hipError_t launch_gemv_mfma_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
+                                  const int64_t* ldy_m, const int8_t* aqs, const uint32_t* ads, int64_t K,
+                                  int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream);
+// Waves per workgroup the matrix-core GEMV gives an N-row matrix (its rows'
+// summation order); matrices with equal counts can share a launch.
+int gemv_mfma_waves(int64_t N);
+
 // Y[i] = W[i] x for i < count <= GEMV_GROUP_MAX, M <= GEMV_MAX_COLS columns
 // of planar Q8_1 activations; Y[i] in ggml layout [M][N[i]] (layout_mk) or
-// [N[i]][M].  One launch when the tile kernel takes the shape, otherwise one
-// per matrix; outputs are bit-identical to launch_gemv on each matrix.
+// [N[i]][M].  The matrices that launch_gemv runs on the matrix cores share a
+// launch per wave count, the others one tile-kernel launch (one launch per
+// matrix where the tile kernel does not take the shape); outputs are
+// bit-identical to launch_gemv on each matrix.
 hipError_t launch_gemv_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N,
                              const int8_t* aqs, const uint32_t* ads, int64_t K, int64_t M, bool layout_mk,
                              hipStream_t stream);

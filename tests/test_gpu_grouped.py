@@ -27,6 +27,11 @@ GROUP_CASES = [  # K, Ns, M, layout
     (2048, (7, 130, 1, 64), 3, LAYOUT_KM),        # ragged last tiles, N = 1
     (17408, (5120, 96), 8, LAYOUT_MK),            # matrix-core GEMV for the wide one, dot4 for the other
     (5120, (8192, 1024, 1024), 6, LAYOUT_KM),
+    (5120, (17408, 17408), 8, LAYOUT_MK),         # gate/up: one matrix-core launch (8 waves each)
+    (5120, (17408, 17408), 4, LAYOUT_KM),
+    (5120, (8192, 4096, 1024), 7, LAYOUT_MK),     # two matrix-core matrices (16 waves) share a launch
+    (5120, (17408, 8192, 2048, 512), 5, LAYOUT_KM),  # 8- and 16-wave launches, one tile launch
+    (2048, (2048 + 7, 4096 + 31), 8, LAYOUT_MK),  # ragged last row blocks in a shared launch
     (8192, (5120,), 2, LAYOUT_KM),
     (1024, (40, 33, 9), 2, LAYOUT_MK),            # K < 2048: one launch per matrix
     (2048, (300, 64), 20, LAYOUT_MK),             # M > 8: one GEMM launch
