@@ -1065,12 +1065,14 @@ static hipError_t launch_flat_depth(const uint8_t* W, const int8_t* aqs, const u
 // does not grow with the columns, the dot4 kernels' does.  Measured on the
 // graph-replayed decode set (K 5120-17408): from 4 columns on it wins on a
 // layer (bs = 4: 2.10 against 2.01 TB/s); below that, and for narrow matrices
-// (k/v, N = 1024: too few 32-row blocks to fill the chip), the dot4 kernels
-// are faster.  Grouped launches use the same rule per matrix, so their
-// outputs match single calls bit for bit.
+// (k/v, N = 1024: too few 32-row blocks to fill the chip) below 8 columns,
+// the dot4 kernels are faster.  Grouped launches use the same rule per
+// matrix, so their outputs match single calls bit for bit.
 static bool use_gemv_mfma(int64_t N, int64_t M) {
     static const int min_cols = tuning_knob("IQ4XS_GEMV_MFMA_MIN_COLS", 4, 1, 9);
-    return M >= min_cols && N >= 2048;
+    // narrow matrices from 8 columns on: k/v (N = 1024) measured 6.60 us
+    // there against 7.05 for dot4 (dot4 wins at 4 and 6 columns)
+    return M >= min_cols && (N >= 2048 || (M >= 8 && N >= 1024));
 }
 
 // X == nullptr: planar Q8_1 activations (aqs, ads); otherwise fp32 X quantised

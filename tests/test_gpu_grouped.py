@@ -30,6 +30,7 @@ GROUP_CASES = [  # K, Ns, M, layout
     (5120, (17408, 17408), 8, LAYOUT_MK),         # gate/up: one matrix-core launch (8 waves each)
     (5120, (17408, 17408), 4, LAYOUT_KM),
     (5120, (8192, 4096, 1024), 7, LAYOUT_MK),     # two matrix-core matrices (16 waves) share a launch
+    (5120, (8192, 1024, 1024), 8, LAYOUT_MK),     # at 8 columns the narrow k/v join q's launch
     (5120, (17408, 8192, 2048, 512), 5, LAYOUT_KM),  # 8- and 16-wave launches, one tile launch
     (2048, (2048 + 7, 4096 + 31), 8, LAYOUT_MK),  # ragged last row blocks in a shared launch
     (8192, (5120,), 2, LAYOUT_KM),
