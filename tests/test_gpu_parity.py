@@ -201,7 +201,9 @@ GEMV_CASES = [(256, 1, 1), (768, 7, 1), (1024, 64, 1), (5120, 333, 1), (4096, 40
               # N >= 2048 and M >= 5: the matrix-core GEMV (ragged last 32-row block; fewer
               # super-blocks than waves; long K; 16- and 8-wave workgroups)
               (2048, 2048 + 33, 6), (768, 2051, 7), (5120, 2048, 8), (17408, 2080, 7), (5120, 8192, 5),
-              (2048, 17408, 5), (5120, 2048 + 5, 4)]
+              (2048, 17408, 5), (5120, 2048 + 5, 4),
+              # from M = 8 also narrow matrices (N >= 1024), at least 8 rows per workgroup
+              (5120, 1024, 8), (2048, 1024 + 17, 8), (768, 1500, 8)]
 
 
 @pytest.mark.parametrize("K,N,M", GEMV_CASES)
