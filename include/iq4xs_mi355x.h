@@ -250,7 +250,8 @@ int iq4xs_mul_mat_q8_1(const void* W, const void* ws, float* Y, int64_t K, int64
  * `layout` selects.  For M <= 8 one launch of the streaming GEMV covers
  * every matrix (q/k/v, gate/up of a decode step) and pays the per-launch
  * fixed cost once; the matrices that take the matrix-core GEMV (M >= 4 and
- * N >= 2048) share one launch of it per wave count (the count follows N),
+ * N >= 2048, or M == 8 and N >= 1024) share one launch of it per wave count
+ * (the count follows N),
  * the others one launch of the streaming GEMV.  For M > 8 one GEMM launch, whose
  * small matrices fill the CUs that the big ones' last round of tiles leaves
  * idle (a short last round lying in the last matrix is a second launch of
