@@ -4,9 +4,10 @@ work and synchronisation between the replays.  Every replay must give the
 eager run's outputs bit for bit (the outputs are overwritten with NaN before
 each replay, so a node that did not run would show).  Covered: the fused
 single-column GEMV (two- and five-round prologues), the quantiser + GEMM,
-the quantiser + matrix-core small-batch GEMV, a grouped GEMV, the rms-fused
-grouped GEMV, the rms + gate/up + SwiGLU launch and the down GEMV on its
-output, the allocation-free entry point and the ggml GEMV hook.  None of
+the quantiser + matrix-core small-batch GEMV, grouped GEMVs (tile and
+matrix-core), the rms-fused grouped GEMV, the rms + gate/up + SwiGLU launch
+and the down GEMV on its output, the allocation-free entry point and the
+ggml GEMV hook.  None of
 them records a memset or an allocation into the graph."""
 import numpy as np
 import pytest
@@ -43,9 +44,10 @@ def test_graph_replays_match_eager(pkg, dev):
         gamma = (torch.rand(H, generator=g) + 0.5).to(dev)
         xff = torch.randn(FF, generator=g).to(dev)
         X4 = torch.randn((4, H), generator=g).to(dev)
+        X8 = torch.randn((8, H), generator=g).to(dev)
         X64 = torch.randn((64, H), generator=g).to(dev)
         ws = {k: pkg.workspace(K, M, dev) for k, (K, M) in
-              {"q": (H, 1), "d": (FF, 1), "m4": (H, 4), "m64": (H, 64), "s": (FF, 1)}.items()}
+              {"q": (H, 1), "d": (FF, 1), "m4": (H, 4), "m8": (H, 8), "m64": (H, 64), "s": (FF, 1)}.items()}
         out = {"q": torch.empty(Q, device=dev), "d": torch.empty(H, device=dev),
                "m4": torch.empty((4, Q), device=dev), "m64": torch.empty((64, Q), device=dev),
                "gq": torch.empty(Q, device=dev), "gk": torch.empty(1024, device=dev),
@@ -53,7 +55,10 @@ def test_graph_replays_match_eager(pkg, dev):
                "h1": torch.empty(H, device=dev), "h2": torch.empty(H, device=dev),
                "S": torch.empty(FF, device=dev), "gate": torch.empty(FF, device=dev),
                "up": torch.empty(FF, device=dev), "down": torch.empty(H, device=dev),
-               "noalloc": torch.empty(1024, device=dev), "hook": torch.empty(1024, device=dev)}
+               "noalloc": torch.empty(1024, device=dev), "hook": torch.empty(1024, device=dev),
+               "g8q": torch.empty((8, Q), device=dev), "g8k": torch.empty((8, 1024), device=dev),
+               "g8v": torch.empty((8, 1024), device=dev), "g4g": torch.empty((4, FF), device=dev),
+               "g4u": torch.empty((4, FF), device=dev)}
 
         def step():
             pkg.mul_mat(Wq, x, H, Q, 1, ws=ws["q"], out=out["q"])             # fused, two rounds
@@ -61,6 +66,11 @@ def test_graph_replays_match_eager(pkg, dev):
             pkg.mul_mat(Wq, X4, H, Q, 4, ws=ws["m4"], out=out["m4"])          # quantiser + matrix-core GEMV
             pkg.mul_mat(Wq, X64, H, Q, 64, ws=ws["m64"], out=out["m64"])      # quantiser + GEMM
             pkg.mul_mat_q8_1_group([Wq, Wk], ws["q"], H, [Q, 1024], 1, outs=[out["gq"], out["gk"]])
+            # matrix-core GEMV groups: q/k/v in one launch at 8 columns, gate/up in one at 4
+            pkg.quantize_q8_1(X8, H, 8, ws=ws["m8"])
+            pkg.mul_mat_q8_1_group([Wq, Wk, Wk], ws["m8"], H, [Q, 1024, 1024], 8,
+                                   outs=[out["g8q"], out["g8k"], out["g8v"]])
+            pkg.mul_mat_q8_1_group([Wg, Wu], ws["m4"], H, [FF, FF], 4, outs=[out["g4g"], out["g4u"]])
             pkg.rms_norm_mul_mat_group([Wq, Wk], x, H, [Q, 1024], residual=r, out_h=out["h1"], gamma=gamma,
                                        outs=[out["rq"], out["rk"]])
             pkg.rms_norm_mul_mat_swiglu(Wg, Wu, out["h1"], H, FF, residual=x, out_h=out["h2"], gamma=gamma,
