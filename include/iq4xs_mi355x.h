@@ -109,7 +109,8 @@ int gemv_iq4xs_gfx1100_gpu(const void* W, const float* x, float* y, int64_t K, i
  * gemm_iq4xs_stream_tiled_gpu (impl_gemm_wmma_stream.hip:321-364),
  * gemm_iq4xs_wmma_gpu / gemm_iq4xs_tiled_gpu (impl_gemm_wmma.hip:199-242).
  * Same signature and layout as gemm_iq4xs_stock_dp4a_gpu (X [K][M], Y [N][M]),
- * same argument checks.  They run this library's int8 GEMM on Q8_1 activations:
+ * same argument checks.  They run this library's matrix-core GEMM on Q8_1
+ * activations (exact integer sub-block sums, the reference's Q8_1 semantics):
  * the reference's fp16 numerics (dequantised weights x fp16-cast activations)
  * are not reproduced. */
 int gemm_iq4xs_wmma_stream_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
@@ -275,7 +276,10 @@ int iq4xs_mul_mat(const void* W, const float* X, float* Y, int64_t K, int64_t N,
 
 /* iq4xs_mul_mat without a workspace argument and without any allocation: the
  * Q8_1 workspace is a static device array of IQ4XS_NOALLOC_SCRATCH_BYTES held
- * by the library (one per GPU, for the life of the process).  No counterpart
+ * by the library (one per GPU, for the life of the process).  The array is part
+ * of the library's code object, so every process that runs any kernel of this
+ * library on a GPU holds those 128 MiB of that GPU's memory, whether or not it
+ * ever calls iq4xs_mul_mat_noalloc.  No counterpart
  * in the reference; for callers that cannot allocate -- code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc.  Same results
  * as iq4xs_mul_mat bit for bit.  IQ4XS_ERROR_INVALID_VALUE when

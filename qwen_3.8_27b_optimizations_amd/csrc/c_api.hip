@@ -228,8 +228,8 @@ int gemm_iq4xs_stock_gpu(const void* W, const float* X, float* Y, int64_t K, int
 }
 
 // The reference's fp16-WMMA GEMM family and its tiled fallbacks share one
-// signature (X [K][M], Y [N][M]); here they all run the int8 GEMM on Q8_1
-// activations, the same kernel as gemm_iq4xs_stock_dp4a_gpu.
+// signature (X [K][M], Y [N][M]); here they all run the matrix-core GEMM on
+// Q8_1 activations, the same kernel as gemm_iq4xs_stock_dp4a_gpu.
 int gemm_iq4xs_wmma_stream_gpu(const void* W, const float* X, float* Y, int64_t K, int64_t N, int64_t M,
                                void* stream) {
     return mul_mat_pooled(W, X, Y, K, N, M, LAYOUT_KM, as_stream(stream));

@@ -5,56 +5,17 @@
 // where sumi is the exact int32 dot of a 32-weight sub-block with the
 // matching Q8_1 block.
 //
-// Default kernel: gemm_f16_kernel (128x128 tile, 8 waves, two LDS stages),
+// The kernel: gemm_f16_kernel (128x128 tile, 8 waves, two LDS stages),
 // which runs the integer products on v_mfma_f32_32x32x16_f16 -- codebook
 // values and Q8_1 codes are exact in fp16 and a sub-block's 32-term sum is an
 // integer below 2^24, so the MFMA returns sumi exactly, as a float -- and
 // leaves one FMA per output and sub-block for the epilogue.  Its design notes
 // are with the kernel below.
 //
-// The int8 kernels below it, gemm_iq4xs_db_kernel (128x128 tile, 16 waves,
-// double-buffered LDS) and gemm_iq4xs_mfma_kernel (64x64 tile, 4 waves,
-// three per CU), run the products on v_mfma_i32_32x32x32_i8 and need a
-// convert as well as the FMA per output and sub-block; they serve K beyond
-// the fp16 kernel's 32-bit offsets and stay selectable for comparison
-// (IQ4XS_GEMM_KIND = 0 / 1 / -1).  Notes on them:
-//
-// Both are VALU-issue bound.  Every output needs its own scale per sub-block,
-// d_w[n] * d_x[m], so the epilogue costs VALU work per output and sub-block
-// against 1/16 of a 32x32x32 int8 MFMA per lane.  The scale tile is formed by
-// a bf16 MFMA from exact hi/lo splits of the two scales (scale_outer2), which
-// leaves 2 VALU ops per output and sub-block (convert, fused add) instead of
-// 3 and removes the per-lane row-scale LDS reads: in the 128x128 kernel 8-20 %
-// faster than the multiply version.  The 64x64 kernel measured 3-5 % slower
-// with it than with the multiplies, but uses it too: both kernels then give
-// bit-identical outputs, so the tile choice (which depends on the shape, and
-// for grouped launches on the group) never changes a result.
-//
-// Measured on the 128x128 kernel with the multiply epilogue: removing the
-// int8 MFMA changed little and every VALU op removed showed up in full; an
-// f32 MFMA (32x32x2) for the same outer product cost as much as the 16
-// multiplies; keeping (ls - 32) as int8 with d_w applied once per super-block
-// (exact int32 sumi*(ls-32)) was 4-8 % slower.
-//
-// Non-finite scales (an fp16 d of Inf/NaN) give NaN in the int8 kernels where
-// the reference's product would give +-Inf: the hi/lo split of an infinite
-// scale is Inf + NaN.  The fp16 kernel keeps the reference's +-Inf: no
-// infinite half of one scale meets a zero half of the other.
-//
-// MI355X mapping (64x64 int8 kernel).  A workgroup (4 waves) owns a 64-row x
-// 64-token output tile and walks K one 256-weight super-block at a time:
-//   1. the 64 weight rows' super-blocks are decoded (v_perm codebook lookup,
-//      decode_codes_x)
-//      straight into int8 LDS tiles, the per-sub-block weight scales
-//      d*(ls-32) into a table of exact bf16 hi/lo pairs (bf16_pair);
-//   2. the 64 tokens' Q8_1 codes are copied to LDS, their d into a pair table;
-//   3. each wave issues one v_mfma_i32_32x32x32_i8 per 32-wide sub-block --
-//      K=32 is exactly one sub-block, so the MFMA result IS the reference's
-//      int32 sumi -- and folds it into fp32 accumulators with the scale tile
-//      of scale_outer2.
-// LDS rows are 256 bytes; the 16-byte chunk index is XORed with (row & 15)
-// so the 32 lanes that read one k-chunk of 32 different rows hit 16
-// distinct chunk positions (no bank conflicts from the 256-byte row stride).
+// Non-finite scales keep the reference's class: the scale tile never puts an
+// infinite half of one scale against a zero half of the other, and a token
+// block whose activation scale d_x is not finite is recomputed term by term
+// with the reference's arithmetic (nonfinite_fixup below).
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -71,15 +32,10 @@
 
 namespace iq4xs {
 
-constexpr int GEMM_BN = 64;  // weight rows per workgroup
-constexpr int GEMM_BM = 64;  // tokens per workgroup
-
-__device__ inline int lds_swz(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
-
-// MFMA 32x32x32 i8 operand / result layout used throughout:
-//   A: lane l supplies row (l & 31), k = 16*(l >> 5) .. +15
-//   B: lane l supplies column (l & 31), k = 16*(l >> 5) .. +15
+// 32x32 MFMA result layout (v_mfma_f32_32x32x16_f16 here, and the
+// v_mfma_i32_32x32x32_i8 of the small-batch GEMV and the layout probe):
 //   C: element e of lane l is row 8*(e>>2) + 4*(l>>5) + (e&3), column (l & 31)
+// (i8 operands: lane l supplies row / column l & 31, k = 16*(l >> 5) .. +15)
 __device__ inline int mfma_c_row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
 
 // Up to GEMV_GROUP_MAX matrices with the same K and the same quantised
@@ -93,360 +49,7 @@ struct GemmGroup {
     int tile_end[GEMV_GROUP_MAX];
 };
 
-// This workgroup's matrix and its first N-tile, by scalar selects on the
-// by-value descriptor (no dynamic index into the argument block).
-template <bool kGroup>
-__device__ inline void gemm_select(const GemmGroup& grp, const uint8_t*& W, float*& Y, int64_t& N, int64_t& ldy_m,
-                                   int& tile0) {
-    W = grp.W[0];
-    Y = grp.Y[0];
-    N = grp.N[0];
-    ldy_m = grp.ldy_m[0];
-    tile0 = 0;
-    if (kGroup) {
-        int g = 0;
-#pragma unroll
-        for (int i = 0; i + 1 < GEMV_GROUP_MAX; ++i) g += (int)blockIdx.x >= grp.tile_end[i] ? 1 : 0;
-#pragma unroll
-        for (int i = 1; i < GEMV_GROUP_MAX; ++i) {
-            if (g == i) {
-                W = grp.W[i];
-                Y = grp.Y[i];
-                N = grp.N[i];
-                ldy_m = grp.ldy_m[i];
-                tile0 = grp.tile_end[i - 1];
-            }
-        }
-    }
-}
-
-typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-
-// x = hi + lo exactly, as two bf16 halves (hi | lo << 16), for any finite x
-// with at most 16 significant bits: d_w * (ls - 32) (11 + 5 bits) and the
-// fp16 d_x both qualify.  hi keeps the top 8 bits, lo the rest.
-__device__ inline uint32_t bf16_pair(float x) {
-    const uint32_t hb = __builtin_bit_cast(uint32_t, x) & 0xFFFF0000u;
-    const float lo = x - __builtin_bit_cast(float, hb);
-    return (hb >> 16) | (__builtin_bit_cast(uint32_t, lo) & 0xFFFF0000u);
-}
-
-// Scale products d_w[row] * d_x[col] of every element of the 32x32 tiles of
-// two sub-blocks s, s+1, in the int8 MFMA's C layout, from two
-// v_mfma_f32_32x32x8_bf16.  pa holds the bf16 pairs of this lane's row scale
-// for s (low dword) and s+1 (high dword); pb0 / pb1 those of its column's.
-// Lane half h supplies k = 4h..4h+3: A = (w_hi, w_lo) of s, then of s+1; B =
-// x_hi (h = 0) or x_lo (h = 1) of s twice, then two zeros (for s; the other
-// way round for s+1), the copy picked by the per-lane selector bsel.  The four
-// nonzero products hi*hi, lo*hi, hi*lo, lo*lo are exact in fp32, so each tile
-// holds d_w * d_x to within fp32 rounding of their sum.  This replaces 16
-// multiplies and 16 row-scale LDS reads per lane and sub-block at one v_perm.
-__device__ inline void scale_outer2(v2u pa, uint32_t pb0, uint32_t pb1, uint32_t bsel, v16f& sc0, v16f& sc1) {
-    const v2u b0 = {__builtin_amdgcn_perm(pb0, pb0, bsel), 0u};
-    const v2u b1 = {0u, __builtin_amdgcn_perm(pb1, pb1, bsel)};
-    sc0 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4s, pa), __builtin_bit_cast(v4s, b0), v16f{}, 0,
-                                                   0, 0);
-    sc1 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(v4s, pa), __builtin_bit_cast(v4s, b1), v16f{}, 0,
-                                                   0, 0);
-}
-
-template <bool kDebug, bool kGroup>
-__global__ __launch_bounds__(256) void gemm_iq4xs_mfma_kernel(const GemmGroup grp, const int8_t* __restrict__ aqs,
-                                                              const uint32_t* __restrict__ ads, int64_t K, int64_t M,
-                                                              int64_t ldy_n, int32_t* __restrict__ dbg) {
-    __shared__ __attribute__((aligned(16))) int8_t sW[GEMM_BN * 256];
-    __shared__ __attribute__((aligned(16))) int8_t sX[GEMM_BM * 256];
-    __shared__ __attribute__((aligned(16))) uint32_t sA[4][GEMM_BN][2];  // bf16 pairs of d_w * (ls - 32), sub-block pairs
-    __shared__ __attribute__((aligned(16))) uint32_t sB[8][GEMM_BM];     // bf16 pairs of d_x
-    __shared__ int sL[kDebug ? 8 : 1][GEMM_BN];  // ls - 32, only for the debug export
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wn = wave & 1, wm = wave >> 1;
-    const uint8_t* W;
-    float* Y;
-    int64_t N, ldy_m;
-    int tile0;
-    gemm_select<kGroup>(grp, W, Y, N, ldy_m, tile0);
-    const int64_t n0 = (int64_t)((int)blockIdx.x - tile0) * GEMM_BN;
-    const int64_t m0 = (int64_t)blockIdx.y * GEMM_BM;
-    const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
-
-    float acc[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-
-    // This thread's share of a super-block's global loads, held in registers:
-    // the next super-block is in flight during the current MFMA phase (a lone
-    // workgroup on a CU, as for k/v-sized grids, would otherwise wait one DRAM
-    // round trip per super-block).  Rows / tokens past the end are clamped.
-    struct Pref64 {
-        uint2 h[2];
-        v4i w[2];
-        v4i x[4];
-        uint32_t ds[2];
-    };
-    auto load = [&](Pref64& g, int64_t kb) {
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int p = tid + 256 * it;
-            const int r = p >> 3, s = p & 7;
-            const int64_t n = (n0 + r < N) ? n0 + r : N - 1;
-            const uint8_t* blk = W + n * row_bytes + kb * BLOCK_BYTES;
-            g.h[it] = *reinterpret_cast<const uint2*>(blk);
-            g.w[it] = *reinterpret_cast<const v4i_a8*>(blk + 8 + 16 * s);
-        }
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int p = tid + 256 * it;
-            const int r = p >> 4, c = p & 15;
-            const int64_t m = (m0 + r < M) ? m0 + r : M - 1;
-            g.x[it] = *reinterpret_cast<const v4i*>(aqs + m * K + kb * QK_K + 16 * c);
-        }
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int p = tid + 256 * it;
-            const int r = p >> 3, s = p & 7;
-            const int64_t m = (m0 + r < M) ? m0 + r : M - 1;
-            g.ds[it] = ads[m * nb + kb * 8 + s];
-        }
-    };
-    Pref64 g;
-    load(g, 0);
-
-    for (int64_t kb = 0; kb < bpr; ++kb) {
-        __syncthreads();
-        // 1. weights: 64 rows x 8 sub-blocks, two (row, sub-block) pairs per thread
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int p = tid + 256 * it;
-            const int r = p >> 3, s = p & 7;
-            const uint2 h = g.h[it];
-            const v4i w = g.w[it];
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)w[j], lo[j], hi[j]);
-            *reinterpret_cast<v4i*>(sW + lds_swz(r, 2 * s)) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
-            *reinterpret_cast<v4i*>(sW + lds_swz(r, 2 * s + 1)) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-            sA[s >> 1][r][s & 1] = bf16_pair(half_bits_to_float(h.x & 0xFFFFu) * (float)(subblock_ls(h.x, h.y, s) - 32));
-            if (kDebug) sL[s][r] = subblock_ls(h.x, h.y, s) - 32;
-        }
-        // 2. activations: 64 tokens x 16 chunks of 16 codes, four per thread
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int p = tid + 256 * it;
-            const int r = p >> 4, c = p & 15;
-            *reinterpret_cast<v4i*>(sX + lds_swz(r, c)) = g.x[it];
-        }
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int p = tid + 256 * it;
-            const int r = p >> 3, s = p & 7;
-            sB[s][r] = bf16_pair(half_bits_to_float(g.ds[it] & 0xFFFFu));
-        }
-        __syncthreads();
-        if (kb + 1 < bpr) load(g, kb + 1);  // in flight during the MFMA phase
-
-        // 3. one int8 MFMA per sub-block; the scale tiles of two sub-blocks
-        //    from two bf16 MFMAs (scale_outer2), exactly as in the 128x128
-        //    kernel, so that both kernels give bit-identical outputs and the
-        //    tile choice never changes a result
-        const int ra = 32 * wn + (lane & 31);
-        const int rb = 32 * wm + (lane & 31);
-        const uint32_t bsel = (lane >> 5) ? 0x03020302u : 0x01000100u;
-#pragma unroll 1
-        for (int s = 0; s < 8; s += 2) {
-            v16f sc[2];
-            scale_outer2(*reinterpret_cast<const v2u*>(&sA[s >> 1][ra][0]), sB[s][rb], sB[s + 1][rb], bsel, sc[0], sc[1]);
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int ch = 2 * (s + u) + (lane >> 5);
-                const v4i a = *reinterpret_cast<const v4i*>(sW + lds_swz(ra, ch));
-                const v4i b = *reinterpret_cast<const v4i*>(sX + lds_swz(rb, ch));
-                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int i = 32 * wn + mfma_c_row(e, lane);
-                    acc[e] += sc[u][e] * (float)c[e];
-                    if (kDebug) {
-                        const int64_t n = n0 + i, m = m0 + rb;
-                        if (n < N && m < M) dbg[(m * N + n) * nb + kb * 8 + s + u] = c[e] * sL[s + u][i];
-                    }
-                }
-            }
-        }
-    }
-
-    const int64_t m = m0 + 32 * wm + (lane & 31);
-    if (m < M) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int64_t n = n0 + 32 * wn + mfma_c_row(e, lane);
-            if (n < N) Y[m * ldy_m + n * ldy_n] = acc[e];
-        }
-    }
-}
-
-// ---------------------------------------------------------------- 128 x 128 double-buffered kernel
-// 16 waves own a 128-row x 128-token tile; wave w computes the 32x32 block at
-// rows 32*(w&3), tokens 32*(w>>2) (one MFMA per 32-wide sub-block).  LDS holds
-// two stages; while the waves run the MFMAs and the scale epilogue of
-// super-block kb from one stage, the global loads of super-block kb+1 are in
-// flight, and they are decoded into the other stage afterwards: one barrier
-// per super-block.  Rows are padded to 272 bytes instead of swizzled: the 16
-// lanes of a ds_read_b128 phase still hit 16 distinct 16-byte bank groups
-// (272*r mod 256 = 16*r), and the address of sub-block s is a constant
-// offset from sub-block 0 (no per-sub-block address arithmetic).
-constexpr int G2_BN = 128, G2_BM = 128, G2_THREADS = 1024;
-constexpr int G2_ROW = 272;                                  // padded LDS row (256 codes + 16)
-// Stage layout: the two scale tables first, then the code tiles, so that every
-// read of the MFMA phase is a 16-bit immediate offset from the stage base.
-constexpr int G2_W_BYTES = G2_BN * G2_ROW, G2_X_BYTES = G2_BM * G2_ROW;
-constexpr int G2_SA_OFF = 0;                                 // uint32 [4][128][2]: bf16 pairs of d_w * (ls - 32)
-constexpr int G2_SB_OFF = G2_SA_OFF + 8 * G2_BN * 4;        // uint32 [8][128]: bf16 pairs of d_x
-constexpr int G2_W_OFF = G2_SB_OFF + 8 * G2_BM * 4;         // int8 [128][272] weight codes
-constexpr int G2_X_OFF = G2_W_OFF + G2_W_BYTES;             // int8 [128][272] token codes
-constexpr int G2_SL_OFF = G2_X_OFF + G2_X_BYTES;            // int8  [8][128] (debug only)
-constexpr int G2_STAGE = G2_SL_OFF;                          // bytes per stage without the debug table
-static_assert(G2_X_OFF + 7 * 32 + 16 < 65536, "MFMA-phase LDS immediate offsets fit 16 bits");
-constexpr int G2_STAGE_DBG = G2_SL_OFF + 8 * G2_BN;
-
-struct GemmPref {
-    v4i wq;
-    v2u wh;
-    v4i x[2];
-    uint32_t ds;
-};
-
-template <bool kDebug, bool kGroup>
-__global__ __launch_bounds__(G2_THREADS) void gemm_iq4xs_db_kernel(const GemmGroup grp, const int8_t* __restrict__ aqs,
-                                                                   const uint32_t* __restrict__ ads, int64_t K,
-                                                                   int64_t M, int64_t ldy_n,
-                                                                   int32_t* __restrict__ dbg) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int kStage = kDebug ? G2_STAGE_DBG : G2_STAGE;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wn = wave & 3, wm = wave >> 2;
-    const uint8_t* W;
-    float* Y;
-    int64_t N, ldy_m;
-    int tile0;
-    gemm_select<kGroup>(grp, W, Y, N, ldy_m, tile0);
-    const int64_t n0 = (int64_t)((int)blockIdx.x - tile0) * G2_BN;
-    const int64_t m0 = (int64_t)blockIdx.y * G2_BM;
-    const int64_t bpr = K / QK_K, nb = K / QK8_1, row_bytes = bpr * BLOCK_BYTES;
-
-    // this thread's share of a super-block's loads (rows / tokens past the end
-    // are clamped to the last one; their results are never stored).  Each is a
-    // 32-bit lane offset from a workgroup-uniform base (the launcher bounds the
-    // tile's span below 2^32 bytes), which keeps the pointers out of VGPRs.
-    const int wr = tid >> 3, wsb = tid & 7;  // weight row, sub-block
-    const uint8_t* wbase = W + n0 * row_bytes;
-    const uint32_t woff = (uint32_t)(((n0 + wr < N) ? wr : N - 1 - n0) * row_bytes);
-    int xr[2], xc[2];
-    uint32_t xoff[2];
-    const int8_t* xbase = aqs + m0 * K;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int p = tid + G2_THREADS * it;
-        xr[it] = p >> 4;
-        xc[it] = p & 15;
-        xoff[it] = (uint32_t)(((m0 + xr[it] < M) ? xr[it] : M - 1 - m0) * K + 16 * xc[it]);
-    }
-    const int dr = tid >> 3, ds_s = tid & 7;  // token, sub-block of the d word
-    const uint32_t* dbase = ads + m0 * nb;
-    const uint32_t doff = (uint32_t)(((m0 + dr < M) ? dr : M - 1 - m0) * nb + ds_s);
-
-    auto load = [&](GemmPref& g, int64_t kb) {
-        const uint8_t* wk = wbase + kb * BLOCK_BYTES;
-        g.wh = *reinterpret_cast<const v2u*>(wk + woff);
-        g.wq = *reinterpret_cast<const v4i_a8*>(wk + woff + 8 + 16 * wsb);
-        const int8_t* xk = xbase + kb * QK_K;
-#pragma unroll
-        for (int it = 0; it < 2; ++it) g.x[it] = *reinterpret_cast<const v4i*>(xk + xoff[it]);
-        g.ds = (dbase + kb * 8)[doff];
-    };
-    auto store = [&](const GemmPref& g, int stage) {
-        uint8_t* base = lds + stage * kStage;
-        uint32_t lo[4], hi[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) decode_codes_x((uint32_t)g.wq[j], lo[j], hi[j]);
-        int8_t* wdst = reinterpret_cast<int8_t*>(base + G2_W_OFF) + wr * G2_ROW + 32 * wsb;
-        *reinterpret_cast<v4i*>(wdst) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
-        *reinterpret_cast<v4i*>(wdst + 16) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        const int ls = subblock_ls(g.wh.x, g.wh.y, wsb) - 32;
-        reinterpret_cast<uint32_t*>(base + G2_SA_OFF)[((wsb >> 1) * G2_BN + wr) * 2 + (wsb & 1)] =
-            bf16_pair(half_bits_to_float(g.wh.x & 0xFFFFu) * (float)ls);
-        if (kDebug) reinterpret_cast<int8_t*>(base + G2_SL_OFF)[wsb * G2_BN + wr] = (int8_t)ls;
-#pragma unroll
-        for (int it = 0; it < 2; ++it)
-            *reinterpret_cast<v4i*>(base + G2_X_OFF + xr[it] * G2_ROW + 16 * xc[it]) = g.x[it];
-        reinterpret_cast<uint32_t*>(base + G2_SB_OFF)[ds_s * G2_BM + dr] = bf16_pair(half_bits_to_float(g.ds & 0xFFFFu));
-    };
-
-    float acc[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-    const int ra = 32 * wn + (lane & 31);
-    const int rb = 32 * wm + (lane & 31);
-    const int half = lane >> 5;  // k = 16*half .. +15 of each 32-wide sub-block
-    const uint32_t bsel = half ? 0x03020302u : 0x01000100u;  // d_x lo (high half) or hi (low half), twice
-
-    GemmPref g;
-    load(g, 0);
-    store(g, 0);
-    __syncthreads();
-    for (int64_t kb = 0; kb < bpr; ++kb) {
-        const int cur = (int)(kb & 1);
-        const bool more = kb + 1 < bpr;
-        if (more) load(g, kb + 1);  // in flight during the MFMA phase
-        const uint8_t* base = lds + cur * kStage;
-        const int8_t* pa = reinterpret_cast<const int8_t*>(base + G2_W_OFF) + ra * G2_ROW + 16 * half;
-        const int8_t* pb = reinterpret_cast<const int8_t*>(base + G2_X_OFF) + rb * G2_ROW + 16 * half;
-        // row-scale pairs of sub-blocks 2t, 2t+1 are adjacent dwords: the table
-        // is [4][128][2] (sub-block pair, row, member)
-        const v2u* pA = reinterpret_cast<const v2u*>(base + G2_SA_OFF) + ra;
-        const uint32_t* pB = reinterpret_cast<const uint32_t*>(base + G2_SB_OFF) + rb;
-#pragma unroll 2
-        for (int s = 0; s < 8; s += 2) {
-            v16f sc[2];
-            scale_outer2(pA[(s >> 1) * G2_BN], pB[s * G2_BM], pB[(s + 1) * G2_BM], bsel, sc[0], sc[1]);
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const v4i a = *reinterpret_cast<const v4i*>(pa + 32 * (s + u));
-                const v4i b = *reinterpret_cast<const v4i*>(pb + 32 * (s + u));
-                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    acc[e] += sc[u][e] * (float)c[e];
-                    if (kDebug) {
-                        const int i = 32 * wn + mfma_c_row(e, lane);
-                        const int8_t* sL = reinterpret_cast<const int8_t*>(base + G2_SL_OFF);
-                        const int64_t m = m0 + rb;
-                        if (m < M && n0 + i < N)
-                            dbg[(m * N + n0 + i) * nb + kb * 8 + s + u] = c[e] * (int)sL[(s + u) * G2_BN + i];
-                    }
-                }
-            }
-        }
-        if (more) store(g, cur ^ 1);
-        __syncthreads();
-    }
-
-    const int64_t m = m0 + rb;
-    if (m < M) {
-        float* yrow = Y + m * ldy_m;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int64_t n = n0 + 32 * wn + mfma_c_row(e, lane);
-            if (n < N) yrow[n * ldy_n] = acc[e];
-        }
-    }
-}
 
 // ---------------------------------------------------------------- fp16 matrix-core kernel
 // The IQ4_XS codebook values (-127..113) and the Q8_1 codes (-127..127) are
@@ -494,13 +97,11 @@ constexpr int kVmcnt5 = 5 | (0x7 << 4) | (0xF << 8);
 
 constexpr int H_BN = 128, H_BM = 128, H_THREADS = 512;
 constexpr int H_ROW = 512;                           // LDS bytes per token row of a super-block
-constexpr int H_T_OFF = H_BM * H_ROW;                // token scale pairs, uint32 [2][128][8]
-constexpr int H_T_COPY = H_BM * 8 * 4;               // copy h of them feeds lane half h
-constexpr int H_STAGE = H_T_OFF + 2 * H_T_COPY;      // 72 KB
 constexpr int H_LUT = 1024;                          // the code pair table
-// The same stage layout for a tile of at most TOK tokens: half-height tiles
-// (64 rows, 4 waves, at most 64 tokens) use TOK = 64, so that two of them
-// fit a CU's LDS.
+// A stage of a tile of at most TOK tokens: the token rows, then the token scale
+// pairs uint32 [2][TOK][8] (copy h feeds lane half h).  Full tiles use TOK =
+// 128 (72 KB); half-height tiles (64 rows, 4 waves, at most 64 tokens) TOK =
+// 64, so that two of them fit a CU's LDS.
 template <int TOK>
 struct HStage {
     static constexpr int t_off = TOK * H_ROW;
@@ -519,24 +120,6 @@ __device__ inline uint32_t bf16_pair_f(float x) {
     const float lo = x - __builtin_bit_cast(float, hb);
     const uint32_t lb = __builtin_isfinite(x) ? (__builtin_bit_cast(uint32_t, lo) & 0xFFFF0000u) : 0u;
     return (hb >> 16) | lb;
-}
-
-// Four int8 codebook values of low nibbles (lo) and of high nibbles (hi) ->
-// four fp16 pair words {lo byte j, hi byte j}, exactly (v_cvt_f16_i16 on a
-// sign-extended byte, written to one half of the word: one op per value).
-__device__ inline v4u kv_pairs_f16(uint32_t lo, uint32_t hi) {
-    uint32_t r0, r1, r2, r3;
-    asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %1, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "v_cvt_f16_i16_sdwa %1, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
-        "v_cvt_f16_i16_sdwa %2, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
-        "v_cvt_f16_i16_sdwa %2, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2\n\t"
-        "v_cvt_f16_i16_sdwa %3, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
-        "v_cvt_f16_i16_sdwa %3, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
-        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
-        : "v"(lo), "v"(hi));
-    return v4u{r0, r1, r2, r3};
 }
 
 // The fp16 code pair word of a qs byte b, {kv[b & 15], kv[b >> 4]}: the
@@ -715,6 +298,58 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
     epilogue(STEPS - 1, dp, sp, 1);
 }
 
+// The outputs of a tile's tokens whose Q8_1 block scale d_x is not finite
+// (|x| >= 65520 * 127 in a 32-block, or a NaN), term by term with the
+// reference's arithmetic (real_stock_dp4a_comparator.hip:164-165):
+// (fp16 d_w * fp16 d_x) * float(sumi * (ls - 32)).  Every output of such a
+// token holds at least one non-finite term, so its value is the fp32 sum of
+// its non-finite terms alone (+-Inf, or NaN for a NaN term or both signs of
+// Inf): a finite term cannot change that sum, and finite partial sums of this
+// format stay far below the fp32 range.  The scale-tile MFMA cannot give this
+// class (an infinite d_x meets the zero k slots of the other sub-blocks), so
+// the tile recomputes these outputs instead.  `flags` is LDS for `toks` ints.
+// Reached only when the tile holds such a token; all threads take part.
+__device__ __noinline__ void nonfinite_fixup(const uint8_t* __restrict__ W, float* __restrict__ Y, int64_t N,
+                                             int64_t ldy_m, int64_t ldy_n, const int8_t* __restrict__ aqs,
+                                             const uint32_t* __restrict__ ads, int64_t K, int64_t M, int64_t n0,
+                                             int rows, int64_t m0, int toks, int* flags) {
+    const int tid = threadIdx.x, nth = blockDim.x;
+    const int64_t nb = K / QK8_1, bpr = K / QK_K;
+    for (int t = tid; t < toks; t += nth) {
+        int bad = 0;
+        if (m0 + t < M)
+            for (int64_t b = 0; b < nb; ++b)
+                bad |= __builtin_isfinite(half_bits_to_float(ads[(m0 + t) * nb + b] & 0xFFFFu)) ? 0 : 1;
+        flags[t] = bad;
+    }
+    __syncthreads();
+    const uint32_t kv[4] = {KV0, KV1, KV2, KV3};
+    auto kval = [&](uint32_t c) { return (int)(int8_t)(kv[c >> 2] >> (8 * (c & 3))); };
+    for (int i = tid; i < toks * rows; i += nth) {
+        const int t = i / rows, r = i % rows;
+        const int64_t m = m0 + t, n = n0 + r;
+        if (!flags[t] || m >= M || n >= N) continue;
+        float y = 0.0f;
+        for (int64_t kb = 0; kb < bpr; ++kb) {
+            const uint8_t* blk = W + (n * bpr + kb) * BLOCK_BYTES;
+            const uint32_t h0 = *reinterpret_cast<const uint32_t*>(blk), h1 = *reinterpret_cast<const uint32_t*>(blk + 4);
+            const float dw = half_bits_to_float(h0 & 0xFFFFu);
+            for (int s = 0; s < 8; ++s) {
+                const float dx = half_bits_to_float(ads[m * nb + kb * 8 + s] & 0xFFFFu);
+                if (__builtin_isfinite(dw) && __builtin_isfinite(dx)) continue;
+                const int8_t* x = aqs + m * K + kb * QK_K + 32 * s;
+                int sumi = 0;
+                for (int j = 0; j < 16; ++j) {
+                    const uint32_t q = blk[8 + 16 * s + j];
+                    sumi += kval(q & 15u) * (int)x[j] + kval(q >> 4) * (int)x[j + 16];
+                }
+                y += (dw * dx) * (float)(sumi * (subblock_ls(h0, h1, s) - 32));
+            }
+        }
+        Y[m * ldy_m + n * ldy_n] = y;
+    }
+}
+
 // One 128-row x 32T-token tile (T token blocks per wave; the per-output
 // arithmetic does not depend on T, so neither do the results).
 // W, Y, N, ldy_m: the tile's matrix, whose first row tile is tile0.
@@ -724,7 +359,8 @@ __device__ __forceinline__ void f16_superblock(const uint8_t* st, const uint8_t*
 // both.
 template <bool kDebug, int T, int RG>
 __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* __restrict__ Y, int64_t N,
-                                         int64_t ldy_m, int tile0, const uint32_t* __restrict__ ahq,
+                                         int64_t ldy_m, int tile0, const int8_t* __restrict__ aqs,
+                                         const uint32_t* __restrict__ ahq,
                                          const uint32_t* __restrict__ ads, int64_t K, int64_t M, int64_t ldy_n, int bx,
                                          int by, uint8_t* smem, int32_t* __restrict__ dbg) {
     static_assert(RG == 4 || (RG == 2 && T <= 2), "half-height tiles hold at most 64 tokens");
@@ -774,10 +410,15 @@ __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* _
     const uint32_t doff = (uint32_t)(((m0 + tm < M) ? tm : M - 1 - m0) * nb + ts);
     auto load_d = [&](int64_t kb) { return *reinterpret_cast<const v2u*>(dtile + kb * 8 + doff); };
     // copy 1 (lane half 1, which meets the weight scale's low half) has 0
-    // for a non-finite d_x, so that no Inf meets a zero low half (0 * Inf)
+    // for a non-finite d_x, so that no Inf meets a zero low half (0 * Inf);
+    // such a token's outputs are recomputed at the end (nonfinite_fixup), and
+    // nf records that this thread saw one among the tile's own tokens
+    const bool own_token = tm < 32 * T && m0 + tm < M;
+    bool nf = false;
     auto store_d = [&](v2u d, uint8_t* stage) {
         uint32_t* t = reinterpret_cast<uint32_t*>(stage + HStage<TOK>::t_off) + tm * 8 + ts;
         const float x0 = half_bits_to_float(d.x & 0xFFFFu), x1 = half_bits_to_float(d.y & 0xFFFFu);
+        nf |= own_token && !(__builtin_isfinite(x0) && __builtin_isfinite(x1));
         const v2u p = v2u{bf16_pair_f(x0), bf16_pair_f(x1)};
         *reinterpret_cast<v2u*>(t) = p;
         *reinterpret_cast<v2u*>(t + HStage<TOK>::t_copy / 4) =
@@ -863,7 +504,7 @@ __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* _
             for (int e = 0; e < 16; ++e) slot(kh, j)[e * 64] = acc[j][e];
         }
     }
-    __syncthreads();
+    const int any_nf = __syncthreads_or(nf ? 1 : 0);
 #pragma unroll
     for (int j = 0; j < T; ++j) {
         if ((j < HALF) == (kh == 0)) {
@@ -871,6 +512,11 @@ __device__ __forceinline__ void f16_tile(const uint8_t* __restrict__ W, float* _
             for (int e = 0; e < 16; ++e) acc[j][e] += slot(kh ^ 1, j)[e * 64];
             store(acc[j], j);
         }
+    }
+    if (any_nf) {  // workgroup-uniform, and only for a token with a non-finite d_x
+        __syncthreads();  // the reduction slots are read above; the fix-up reuses the LDS
+        nonfinite_fixup(W, Y, N, ldy_m, ldy_n, aqs, ads, K, M, n0, 32 * RG, m0, 32 * T,
+                        reinterpret_cast<int*>(&stages[0][0]));
     }
 }
 
@@ -893,7 +539,8 @@ struct F16Plan {
 // tiles of 4 waves and at most 64 tokens (two per CU), for launches with too
 // few big tiles to fill the CUs.  A row's arithmetic is the same in both.
 template <bool kDebug, bool kGroup, int RG = 4>
-__global__ __launch_bounds__(128 * RG) void gemm_f16_kernel(const GemmGroup grp, const uint32_t* __restrict__ ahq,
+__global__ __launch_bounds__(128 * RG) void gemm_f16_kernel(const GemmGroup grp, const int8_t* __restrict__ aqs,
+                                                            const uint32_t* __restrict__ ahq,
                                                             const uint32_t* __restrict__ ads, int64_t K, int64_t M,
                                                             int64_t ldy_n, const F16Plan plan,
                                                             int32_t* __restrict__ dbg) {
@@ -922,7 +569,8 @@ __global__ __launch_bounds__(128 * RG) void gemm_f16_kernel(const GemmGroup grp,
         tile = x * q + min(x, r) + (b >> 3);
     }
     const int bx = sg.rt0 + tile % sg.rts, by = tile / sg.rts;
-    // the matrix of this tile: gemm_select's choice, by the logical tile index
+    // the matrix of this tile, by scalar selects on the by-value descriptor
+    // (no dynamic index into the argument block), from the logical tile index
     const uint8_t* W = grp.W[0];
     float* Y = grp.Y[0];
     int64_t N = grp.N[0], ldy_m = grp.ldy_m[0];
@@ -943,24 +591,16 @@ __global__ __launch_bounds__(128 * RG) void gemm_f16_kernel(const GemmGroup grp,
         }
     }
     if constexpr (RG == 2) {
-        if (sg.T == 1) f16_tile<kDebug, 1, 2>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg);
-        else f16_tile<kDebug, 2, 2>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg);
+        if (sg.T == 1) f16_tile<kDebug, 1, 2>(W, Y, N, ldy_m, tile0, aqs, ahq, ads, K, M, ldy_n, bx, by, smem, dbg);
+        else f16_tile<kDebug, 2, 2>(W, Y, N, ldy_m, tile0, aqs, ahq, ads, K, M, ldy_n, bx, by, smem, dbg);
     } else {
         switch (sg.T) {
-            case 1: f16_tile<kDebug, 1, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
-            case 2: f16_tile<kDebug, 2, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
-            case 3: f16_tile<kDebug, 3, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
-            default: f16_tile<kDebug, 4, 4>(W, Y, N, ldy_m, tile0, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+            case 1: f16_tile<kDebug, 1, 4>(W, Y, N, ldy_m, tile0, aqs, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+            case 2: f16_tile<kDebug, 2, 4>(W, Y, N, ldy_m, tile0, aqs, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+            case 3: f16_tile<kDebug, 3, 4>(W, Y, N, ldy_m, tile0, aqs, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
+            default: f16_tile<kDebug, 4, 4>(W, Y, N, ldy_m, tile0, aqs, ahq, ads, K, M, ldy_n, bx, by, smem, dbg); break;
         }
     }
-}
-
-static int gemm_kind() {
-    static const int kind = []() {
-        const char* v = getenv("IQ4XS_GEMM_KIND");  // tuning override: 0 = 64x64, 1 = 128x128, 2 = fp16 matrix cores
-        return v ? atoi(v) : 2;
-    }();
-    return kind;
 }
 
 // Time of one workgroup of T token blocks relative to T = 4 with every CU
@@ -1073,7 +713,8 @@ static F16Plan f16_plan(int64_t row_tiles, int64_t M) {
 }
 
 template <bool kDebug, bool kGroup>
-static hipError_t launch_f16_kernel(const GemmGroup& grp, int64_t row_tiles, const uint32_t* ahq, const uint32_t* ads,
+static hipError_t launch_f16_kernel(const GemmGroup& grp, int64_t row_tiles, const int8_t* aqs, const uint32_t* ahq,
+                                    const uint32_t* ads,
                                     int64_t K, int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
     if (row_tiles * f16_token_tiles(M, 1) > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     // Half-height tiles (64 rows, 4 waves, one token block each) when even
@@ -1088,149 +729,55 @@ static hipError_t launch_f16_kernel(const GemmGroup& grp, int64_t row_tiles, con
         const F16Plan plan = f16_plan_of({{rt2, 1}}, M);
         const int wgs = plan.seg[F16_SEGS - 1].wg_end;
         if (wgs <= 0) return hipSuccess;
-        hipLaunchKernelGGL((gemm_f16_kernel<false, false, 2>), dim3((unsigned)wgs), dim3(256), 0, stream, g2, ahq,
+        hipLaunchKernelGGL((gemm_f16_kernel<false, false, 2>), dim3((unsigned)wgs), dim3(256), 0, stream, g2, aqs, ahq,
                            ads, K, M, ldy_n, plan, dbg);
         return hipGetLastError();
     }
     const F16Plan plan = kDebug ? f16_plan_of({{row_tiles, 4}}, M) : f16_plan(row_tiles, M);
     const int wgs = plan.seg[F16_SEGS - 1].wg_end;
     if (wgs <= 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_f16_kernel<kDebug, kGroup>), dim3((unsigned)wgs), dim3(H_THREADS), 0, stream, grp, ahq,
+    hipLaunchKernelGGL((gemm_f16_kernel<kDebug, kGroup>), dim3((unsigned)wgs), dim3(H_THREADS), 0, stream, grp, aqs, ahq,
                        ads, K, M, ldy_n, plan, dbg);
     return hipGetLastError();
 }
 
-// The fp16 kernel addresses a tile's weight rows and tokens with 32-bit offsets.
+// The kernel addresses a tile's weight rows and tokens with 32-bit offsets
+// (K below 2^24: far past any matrix of this format in use).
 static bool f16_fits(int64_t K) {
     return (int64_t)H_BN * (K / QK_K) * BLOCK_BYTES < (1ll << 32) && (int64_t)H_BM * 2 * K < (1ll << 32);
-}
-
-// The 128x128 kernel runs one workgroup per CU and is faster per tile; the
-// 64x64 kernel (three per CU) wins when big tiles would leave many CUs idle:
-// fewer tiles than ~9/16 of the CUs (k/v-sized matrices).  Both give
-// bit-identical outputs, so this choice is a speed choice only (thresholds
-// from measurements on the 27B-class shapes at M = 512 / 2048).
-static bool use_big_tiles(int64_t N, int64_t M, int64_t K) {
-    // the 128x128 kernel addresses a tile's rows and tokens with 32-bit offsets
-    if ((int64_t)G2_BN * (K / QK_K) * BLOCK_BYTES >= (1ll << 32) || (int64_t)G2_BM * K >= (1ll << 32)) return false;
-    const int k = gemm_kind();
-    if (k == 0 || k == 1) return k == 1;
-    const int64_t cus = device_cu_count();
-    const int64_t tiles = ((N + G2_BN - 1) / G2_BN) * ((M + G2_BM - 1) / G2_BM);
-    return tiles >= cus * 9 / 16;
-}
-
-template <bool kDebug, bool kGroup>
-static hipError_t launch_gemm_kernel(bool big, const GemmGroup& grp, int64_t gx, const int8_t* aqs, const uint32_t* ads,
-                                     int64_t K, int64_t M, int64_t ldy_n, int32_t* dbg, hipStream_t stream) {
-    const int64_t gy = (M + (big ? G2_BM : GEMM_BM) - 1) / (big ? G2_BM : GEMM_BM);
-    if (gx > 0x7FFFFFFF || gy > 65535) return hipErrorInvalidConfiguration;
-    if (big) {
-        static const bool attrs = []() {
-            // two stages exceed the default dynamic-LDS cap; gfx950 has 160 KB per CU
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_iq4xs_db_kernel<kDebug, kGroup>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      2 * (kDebug ? G2_STAGE_DBG : G2_STAGE));
-            return true;
-        }();
-        (void)attrs;
-        hipLaunchKernelGGL((gemm_iq4xs_db_kernel<kDebug, kGroup>), dim3((unsigned)gx, (unsigned)gy), dim3(G2_THREADS),
-                           2 * (size_t)(kDebug ? G2_STAGE_DBG : G2_STAGE), stream, grp, aqs, ads, K, M, ldy_n, dbg);
-    } else {
-        hipLaunchKernelGGL((gemm_iq4xs_mfma_kernel<kDebug, kGroup>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
-                           stream, grp, aqs, ads, K, M, ldy_n, dbg);
-    }
-    return hipGetLastError();
 }
 
 hipError_t launch_gemm(const uint8_t* W, const int8_t* aqs, const uint32_t* ads, const uint32_t* ahq, float* Y,
                        int64_t K, int64_t N, int64_t M, int64_t ldy_m, int64_t ldy_n, int32_t* dbg,
                        hipStream_t stream) {
     clear_launch_error();
-    if (gemm_kind() == 2 && f16_fits(K)) {
-        GemmGroup grp{};
-        grp.W[0] = W;
-        grp.Y[0] = Y;
-        grp.N[0] = N;
-        grp.ldy_m[0] = ldy_m;
-        const int64_t gx = (N + H_BN - 1) / H_BN;
-        if (gx > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-        grp.tile_end[0] = (int)gx;
-        return dbg ? launch_f16_kernel<true, false>(grp, gx, ahq, ads, K, M, ldy_n, dbg, stream)
-                   : launch_f16_kernel<false, false>(grp, gx, ahq, ads, K, M, ldy_n, dbg, stream);
-    }
-    const bool big = use_big_tiles(N, M, K);
+    if (!f16_fits(K)) return hipErrorInvalidConfiguration;
     GemmGroup grp{};
     grp.W[0] = W;
     grp.Y[0] = Y;
     grp.N[0] = N;
     grp.ldy_m[0] = ldy_m;
-    const int64_t gx = (N + (big ? G2_BN : GEMM_BN) - 1) / (big ? G2_BN : GEMM_BN);
+    const int64_t gx = (N + H_BN - 1) / H_BN;
     if (gx > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     grp.tile_end[0] = (int)gx;
-    if (big && dbg == nullptr) {
-        // Big tiles whose last round on the CUs would hold only a few (at most
-        // a quarter): the rows of that round go to the 64x64 kernel in a
-        // second launch, whose small tiles spread them over the chip.  Both
-        // kernels give bit-identical outputs.  M = 512 gate/up: 544 tiles =
-        // 2 full rounds + 32 on 256 CUs.
-        const int64_t gy = (M + G2_BM - 1) / G2_BM;
-        const int64_t cus = device_cu_count();
-        const int64_t full = gx * gy / cus, rem = gx * gy - full * cus;
-        if (full >= 1 && rem > 0 && 4 * rem <= cus && (full * cus) % gy == 0) {
-            const int64_t gx_big = full * cus / gy;  // whole N-tiles, every token tile
-            const int64_t n_big = gx_big * G2_BN;    // < N, since rem > 0
-            grp.N[0] = n_big;
-            grp.tile_end[0] = (int)gx_big;
-            const hipError_t e = launch_gemm_kernel<false, false>(true, grp, gx_big, aqs, ads, K, M, ldy_n, dbg, stream);
-            if (e != hipSuccess) return e;
-            GemmGroup rest{};
-            rest.W[0] = W + n_big * ((K / QK_K) * BLOCK_BYTES);
-            rest.Y[0] = Y + n_big * ldy_n;
-            rest.N[0] = N - n_big;
-            rest.ldy_m[0] = ldy_m;
-            const int64_t gx_rest = (N - n_big + GEMM_BN - 1) / GEMM_BN;
-            rest.tile_end[0] = (int)gx_rest;
-            return launch_gemm_kernel<false, false>(false, rest, gx_rest, aqs, ads, K, M, ldy_n, dbg, stream);
-        }
-    }
-    return dbg ? launch_gemm_kernel<true, false>(big, grp, gx, aqs, ads, K, M, ldy_n, dbg, stream)
-               : launch_gemm_kernel<false, false>(big, grp, gx, aqs, ads, K, M, ldy_n, dbg, stream);
+    return dbg ? launch_f16_kernel<true, false>(grp, gx, aqs, ahq, ads, K, M, ldy_n, dbg, stream)
+               : launch_f16_kernel<false, false>(grp, gx, aqs, ahq, ads, K, M, ldy_n, dbg, stream);
 }
 
-// One launch for `count` matrices sharing K and the activations (two when a
-// short last round is split off, below): the tile size is chosen for the
-// summed rows, so the small matrices fill CUs that the big ones' last round
-// leaves idle.
+// One launch for `count` matrices sharing K and the activations: the round
+// planner sees the summed row tiles, so the small matrices fill CUs that the
+// big ones' last round leaves idle.
 hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y, const int64_t* N, const int8_t* aqs,
                              const uint32_t* ads, const uint32_t* ahq, int64_t K, int64_t M, bool layout_mk,
                              hipStream_t stream) {
     clear_launch_error();
     if (count < 1 || count > GEMV_GROUP_MAX) return hipErrorInvalidValue;
-    int64_t n_sum = 0;
-    for (int i = 0; i < count; ++i) n_sum += N[i];
-    if (gemm_kind() == 2 && f16_fits(K)) {
-        GemmGroup grp{};
-        int64_t tiles = 0;
-        for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
-            const int j = i < count ? i : count - 1;  // unused entries repeat the last matrix, past every tile
-            if (i < count) tiles += (N[j] + H_BN - 1) / H_BN;
-            if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-            grp.W[i] = W[j];
-            grp.Y[i] = Y[j];
-            grp.N[i] = N[j];
-            grp.ldy_m[i] = layout_mk ? N[j] : 1;
-            grp.tile_end[i] = (int)tiles;
-        }
-        return launch_f16_kernel<false, true>(grp, tiles, ahq, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
-    }
-    const bool big = use_big_tiles(n_sum, M, K);
-    const int bn = big ? G2_BN : GEMM_BN;
+    if (!f16_fits(K)) return hipErrorInvalidConfiguration;
     GemmGroup grp{};
     int64_t tiles = 0;
     for (int i = 0; i < GEMV_GROUP_MAX; ++i) {
         const int j = i < count ? i : count - 1;  // unused entries repeat the last matrix, past every tile
-        if (i < count) tiles += (N[j] + bn - 1) / bn;
+        if (i < count) tiles += (N[j] + H_BN - 1) / H_BN;
         if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
         grp.W[i] = W[j];
         grp.Y[i] = Y[j];
@@ -1238,39 +785,11 @@ hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y
         grp.ldy_m[i] = layout_mk ? N[j] : 1;
         grp.tile_end[i] = (int)tiles;
     }
-    if (big) {
-        // As for single calls: a short last round of big tiles, when it lies
-        // in the last matrix, becomes a 64x64 launch over that matrix's
-        // trailing rows (M = 512 gate+up: 1088 tiles = 4 rounds + 64).
-        const int64_t gy = (M + G2_BM - 1) / G2_BM;
-        const int64_t cus = device_cu_count();
-        const int64_t full = tiles * gy / cus, rem = tiles * gy - full * cus;
-        const int last = count - 1;
-        const int64_t first_last = last > 0 ? grp.tile_end[last - 1] : 0;  // the last matrix's first N-tile
-        if (full >= 1 && rem > 0 && 4 * rem <= cus && (full * cus) % gy == 0 && full * cus / gy > first_last) {
-            const int64_t t_big = full * cus / gy;                 // N-tiles of the grouped launch
-            const int64_t n_keep = (t_big - first_last) * G2_BN;  // rows of the last matrix it keeps (< N)
-            for (int i = last; i < GEMV_GROUP_MAX; ++i) {
-                grp.N[i] = n_keep;
-                grp.tile_end[i] = (int)t_big;
-            }
-            const hipError_t e =
-                launch_gemm_kernel<false, true>(true, grp, t_big, aqs, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
-            if (e != hipSuccess) return e;
-            GemmGroup rest{};
-            rest.W[0] = W[last] + n_keep * ((K / QK_K) * BLOCK_BYTES);
-            rest.Y[0] = Y[last] + n_keep * (layout_mk ? 1 : M);
-            rest.N[0] = N[last] - n_keep;
-            rest.ldy_m[0] = layout_mk ? N[last] : 1;
-            const int64_t gx_rest = (N[last] - n_keep + GEMM_BN - 1) / GEMM_BN;
-            rest.tile_end[0] = (int)gx_rest;
-            return launch_gemm_kernel<false, false>(false, rest, gx_rest, aqs, ads, K, M, layout_mk ? 1 : M, nullptr,
-                                                    stream);
-        }
-    }
-    return launch_gemm_kernel<false, true>(big, grp, tiles, aqs, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
+    return launch_f16_kernel<false, true>(grp, tiles, aqs, ahq, ads, K, M, layout_mk ? 1 : M, nullptr, stream);
 }
 
+// One v_mfma_i32_32x32x32_i8 on a 32x32 A and B (k-contiguous rows), C row-major:
+// pins the operand and result layout that the small-batch matrix-core GEMV uses.
 __global__ __launch_bounds__(64) void probe_mfma_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                         int32_t* __restrict__ C) {
     const int lane = threadIdx.x;

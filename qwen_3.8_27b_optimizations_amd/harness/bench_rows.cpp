@@ -94,14 +94,16 @@ hipError_t lut_no_table(const block_iq4_xs* W, const float* X, float* Y, int64_t
     return gemm_iq4xs_lut_gpu(W, nullptr, X, Y, K, N, M, s);
 }
 // the reference's variant names (bench_gemm_wmma.cpp:89-95) with the entry point
-// each binds; here every one runs the same GEMM (128x128 or 64x64 int8-MFMA tiles
-// chosen per shape, double-buffered LDS, padded / XOR-swizzled rows)
+// each binds; here every one runs the same kernel, gemm_f16_kernel: 128-row x
+// 32-128-token tiles chosen per shape by the round planner (64-row tiles where
+// 128-row ones would leave half the CUs idle), two LDS stages, token rows
+// XOR-swizzled by 16-byte chunk, exact integer products on fp16 MFMA
 const Variant kVariants[] = {
-    {"64x32_P2+33", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_stream_gpu},
-    {"64x32_P4_XOR", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_p4_xor_gpu},
-    {"64x64_P4_XOR", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_64x64_gpu},
-    {"128x32", "128x128|64x64", "P=2", "pad272|xor", gemm_iq4xs_wmma_stream_gpu},
-    {"LUT_mu4", "128x128|64x64", "P=2", "pad272|xor", lut_no_table},
+    {"64x32_P2+33", "128xT32-128|64x32", "P=2", "xor16", gemm_iq4xs_wmma_stream_gpu},
+    {"64x32_P4_XOR", "128xT32-128|64x32", "P=2", "xor16", gemm_iq4xs_wmma_p4_xor_gpu},
+    {"64x64_P4_XOR", "128xT32-128|64x32", "P=2", "xor16", gemm_iq4xs_wmma_64x64_gpu},
+    {"128x32", "128xT32-128|64x32", "P=2", "xor16", gemm_iq4xs_wmma_stream_gpu},
+    {"LUT_mu4", "128xT32-128|64x32", "P=2", "xor16", lut_no_table},
 };
 
 Row gemv_row(const Shape& sh, size_t bytes, const BenchStats& st, const BenchStats& gx) {
@@ -153,8 +155,9 @@ Row gemm_row(const Shape& sh, int64_t M, size_t bytes, double flops, int runs, c
     r.f("speedup", sp, 3).f("speedup_median", sp, 3).f("speedup_vs_stock_dp4a", sp, 3);
     r.f("speedup_mean", sp_mean, 3).f("speedup_mean_minus_1sigma", sp_1s, 3).f("TFLOPS_median", tf, 3);
     r.f("GB/s", wm.gb_s, 2).s("winner", sp > 1.0 ? "wmma_stream" : "stock_dp4a");
-    r.s("note", "MI355X gfx950 int8-MFMA GEMM on Q8_1 activations (the reference's fp16 WMMA numerics are not "
-                "reproduced); every variant name binds this library's GEMM");
+    r.s("note", "MI355X gfx950 gemm_f16_kernel on Q8_1 activations: exact integer sub-block sums on "
+                "v_mfma_f32_32x32x16_f16, one fp32 FMA per output and sub-block (the reference's fp16 WMMA "
+                "numerics are not reproduced); every variant name binds this library's GEMM");
     return r;
 }
 

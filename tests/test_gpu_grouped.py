@@ -36,11 +36,11 @@ GROUP_CASES = [  # K, Ns, M, layout
     (8192, (5120,), 2, LAYOUT_KM),
     (1024, (40, 33, 9), 2, LAYOUT_MK),            # K < 2048: one launch per matrix
     (2048, (300, 64), 20, LAYOUT_MK),             # M > 8: one GEMM launch
-    (5120, (8192, 1024, 1024), 512, LAYOUT_MK),   # q alone takes 128x128 tiles, the group 64x64 ones
-    (5120, (17408, 17408), 512, LAYOUT_KM),       # gate/up: 64x64 alone, 128x128 as a group
+    (5120, (8192, 1024, 1024), 512, LAYOUT_MK),   # q/k/v: the planner sees 80 row tiles, k alone 8
+    (5120, (17408, 17408), 512, LAYOUT_KM),       # gate/up: a bulk of whole rounds and a tail segment
     (8192, (130, 4000, 64), 200, LAYOUT_MK),      # ragged tiles in every matrix
-    # 271 big tiles on 256 CUs: the short last round lies in the second matrix, whose
-    # trailing 1797 rows go to a small-tile launch (token-major outputs, ragged rows)
+    # 271 row tiles on 256 CUs: the planner's tail segment lies in the second matrix
+    # (token-major outputs, ragged rows)
     (256, (128 * 200, 128 * 70 + 5), 100, LAYOUT_KM),
 ]
 

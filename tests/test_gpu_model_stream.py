@@ -11,6 +11,7 @@ GPU, checked against the oracle.
   blocks it read.
 * The full 64-layer bs=1 chain: finite, the four variants bit-identical to
   each other, and a replay bit-identical to the first run.
+* The full 64-layer M=512 pass: finite, grouped bit-identical to plain.
 """
 import numpy as np
 import pytest
@@ -152,4 +153,24 @@ def test_64_layers_bs1_variants_bit_identical(pkg, bench, model, dev):
         for j, (a, b) in enumerate(zip(states["plain"], states[variant])):
             assert np.array_equal(a, b), (variant, j)
     # the chain did run: the last layer's outputs are not the initial zeros
+    assert np.any(states["plain"][-1] != 0)
+
+
+def test_64_layers_bs512_grouped_bit_identical(pkg, bench, model, dev):
+    """The whole-model prefill pass (M = 512 through all 64 layers, producers and the q
+    re-quantisation included): finite, and with the grouped launches (q/k/v and gate/up one
+    iq4xs_mul_mat_q8_1_group each) bit-identical to one call per projection -- the residual
+    stream h after layer 64 and the last layer's seven outputs, which every earlier layer
+    feeds."""
+    stream = torch.cuda.current_stream()
+    states = {}
+    for variant in ("plain", "grouped"):
+        print(f"[model-stream] 64 layers M=512 variant={variant}", flush=True)
+        chain = bench.ModelChain(torch, pkg, pkg.lib(), model, 512, stream, variant)
+        chain.run()
+        assert chain.finite(), variant
+        states[variant] = [bits(t) for t in chain.state()]
+        del chain
+    for j, (a, b) in enumerate(zip(states["plain"], states["grouped"])):
+        assert np.array_equal(a, b), j
     assert np.any(states["plain"][-1] != 0)

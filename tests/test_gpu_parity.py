@@ -297,13 +297,12 @@ def test_fused_rejects_oversized_activations(pkg, dev):
 
 GEMM_CASES = [(256, 64, 64), (256, 1, 1), (512, 100, 20), (768, 130, 65), (1024, 64, 128),
               (2048, 200, 100), (512, 64, 512), (256, 300, 9),
-              # grids of >= 144 tiles of 128x128 take the double-buffered 128x128 kernel
-              # (its debug instantiation included): one super-block per row; then an odd
-              # super-block count with ragged rows and tokens
+              # more row tiles than CUs: one super-block per row; then an odd super-block count
+              # with ragged rows and tokens
               (256, 128 * 148, 64), (768, 128 * 145 + 33, 33),
-              # more than one round of 128x128 tiles on 256 CUs with a short last round: its rows
-              # go to the 64x64 kernel in a second launch (the debug export keeps one launch, so
-              # the equality with it below pins the split bit for bit)
+              # more than one round of 128-row tiles on 256 CUs with a short last round: the round
+              # planner gives the tail smaller token tiles (the debug export keeps one segment of
+              # full tiles, so the equality with it below pins every plan bit for bit)
               (256, 128 * 276 + 5, 100), (256, 128 * 68 + 7, 512)]
 
 
@@ -329,7 +328,7 @@ def test_gemm_sums_and_outputs(pkg, orc, dev, K, N, M):
 EXTREME_D = np.array([0x0000, 0x0001, 0x0400, 0x3C00, 0x7BFF, 0x8400, 0x8001, 0xFBFF], np.uint16)
 
 
-# N, M: bs=1 tile GEMV, matrix-core GEMV (M = 4, 8), 64x64 GEMM, 128x128 GEMM (146 tiles)
+# N, M: bs=1 tile GEMV, matrix-core GEMV (M = 4, 8), the GEMM on one and on many row tiles
 @pytest.mark.parametrize("N,M", [(2051, 1), (2051, 4), (2051, 8), (2051, 100), (128 * 145 + 3, 64)])
 def test_extreme_weight_scales(pkg, orc, dev, N, M):
     """Each kernel family on weights whose fp16 d spans zero, subnormals and the largest
@@ -453,12 +452,26 @@ def test_config2_small_batch_full_size(pkg, orc, dev, proj, M):
     assert m["rel_l2"] <= REL_L2_TOL and not m["bad"], m
 
 
+def dequantised_activations_km(pkg, ws, K, M):
+    """x_hat = d * q of every Q8_1 block (exact in fp32), as X[k*M + m] on the device."""
+    blk = pkg.q8_1_blocks(ws, K, M)
+    d = blk[:, 0:2].contiguous().view(torch.float16).float()            # [M*K/32, 1]
+    q = blk[:, 4:].contiguous().view(torch.int8).float()                # [M*K/32, 32]
+    return (q * d).reshape(M, K).T.contiguous()
+
+
 @pytest.mark.parametrize("M", [512, 2048])
 @pytest.mark.parametrize("proj", list(CONFIG1))
-def test_config3_prefill_gemm_sampled_rows(pkg, orc, dev, proj, M):
-    """Every config-1 projection at M = 512 and 2048: the shapes' own kernel choices (k/v on
-    the 64x64 kernel, gate/up at M = 512 through the split last round) at their real sizes.
-    The rows sampled include the first and last of the matrix."""
+def test_config3_prefill_gemm_full_size(pkg, orc, dev, proj, M):
+    """Every config-1 projection at M = 512 and 2048, through the plans the round planner
+    picks for these shapes (bulk and tail segments, 64-row tiles for k/v at M = 512).
+    * Sampled rows, the first and last included, against the CPU oracle's reference kernel
+      semantics (rel-L2 1e-4).
+    * Every output against the reference's FP64 comparator (gemm_iq4xs_stock_gpu, pinned bit
+      for bit to ref_cpu.cpp by the golden outputs) evaluated on the dequantised activations
+      x_hat: the two differ by fp32 rounding only, so each weight row and each token is held
+      to rel-L2 1e-4 on its own -- a wrong tile, segment or row anywhere fails -- and the
+      whole output to cosine 0.99999."""
     print(f"config3 {proj} M={M}", flush=True)
     K, N = CONFIG1[proj]
     W = pkg.synthetic_weights(K, N, seed=46, device=dev)
@@ -473,6 +486,20 @@ def test_config3_prefill_gemm_sampled_rows(pkg, orc, dev, proj, M):
     Y_sem = orc.gemm_semantics(sampled_rows(W, N, rows), AQ, K, len(rows), M).T
     m = compute_metrics(Y_sem, Y.cpu().numpy()[:, rows])
     assert m["rel_l2"] <= REL_L2_TOL and not m["bad"], m
+    # every output against FP64 on x_hat
+    Y64 = torch.full((N, M), float("nan"), device=dev)
+    xhat = dequantised_activations_km(pkg, ws, K, M)
+    pkg.lib().check("gemm_iq4xs_stock_gpu", W.data_ptr(), xhat.data_ptr(), Y64.data_ptr(), K, N, M, stream())
+    torch.cuda.synchronize()
+    a, b = Y64.T.double(), Y.double()                                    # [M, N]
+    assert bool(torch.isfinite(b).all()) and bool(torch.isfinite(a).all())
+    err = (a - b).square()
+    per_row = (err.sum(0) / a.square().sum(0)).sqrt()                   # each weight row n
+    per_tok = (err.sum(1) / a.square().sum(1)).sqrt()                   # each token m
+    assert float(per_row.max()) <= REL_L2_TOL, ("row", int(per_row.argmax()), float(per_row.max()))
+    assert float(per_tok.max()) <= REL_L2_TOL, ("token", int(per_tok.argmax()), float(per_tok.max()))
+    cos = float((a * b).sum() / (a.norm() * b.norm()))
+    assert cos >= COS_TOL, cos
 
 
 def test_deterministic_replay(pkg, dev):
@@ -489,10 +516,10 @@ def test_deterministic_replay(pkg, dev):
 
 # Non-finite fp16 super-block scales (+Inf, -Inf, NaN): every output keeps the reference's
 # class (finite within tolerance, +Inf, -Inf or NaN), as the reference's product
-# fp16(d_w) * fp16(d_x) * float(sumi * (ls - 32)) gives it.  An activation block whose Q8_1
-# scale overflows to +Inf (|x| >= 8.3e6) keeps it in the GEMV paths; the fp16 GEMM turns that
-# token's outputs into NaN instead (its scale MFMA meets the Inf with the zero k slots of the
-# other sub-blocks), so it is checked for the GEMV paths only.
+# fp16(d_w) * fp16(d_x) * float(sumi * (ls - 32)) gives it.  So does an activation block whose
+# Q8_1 scale overflows to +Inf (|x| >= 8.3e6): the GEMV paths carry it through, and the GEMM
+# recomputes that token's outputs term by term (its scale MFMA would meet the Inf with the
+# zero k slots of the other sub-blocks).
 NONFINITE_D = np.array([0x7C00, 0xFC00, 0x7E00], np.uint16)
 
 
@@ -534,11 +561,25 @@ def test_nonfinite_weight_scales_keep_reference_classes(pkg, orc, dev, M):
     check_classes(y_ref, Y.cpu().numpy().reshape(M, N), f"non-finite weight scales, M={M}")
 
 
-@pytest.mark.parametrize("M", [4, 8])
-def test_infinite_activation_scale_in_gemv_paths(pkg, orc, dev, M):
+# M: matrix-core GEMV (4, 8) and the GEMM (64: one token tile; 200: more than one), on
+# weights that also carry non-finite scales
+@pytest.mark.parametrize("M", [4, 8, 64, 200])
+def test_infinite_activation_scale_keeps_reference_classes(pkg, orc, dev, M):
+    print(f"Inf d_x M={M}", flush=True)
     K, N, W, X = nonfinite_case(orc, M, inf_activation=True)
     AQ = orc.quantize_q8_1_batched(X, K, M, LAYOUT_MK)
-    ws = pkg.quantize_q8_1(D(X, dev), K, M, LAYOUT_MK)
-    Y = pkg.mul_mat_q8_1(D(W, dev), ws, K, N, M, LAYOUT_MK, pkg.PATH_GEMV)
+    y_ref = orc.gemm_semantics(W, AQ, K, N, M).T
+    Wd, Xd = D(W, dev), D(X, dev)
+    ws = pkg.quantize_q8_1(Xd, K, M, LAYOUT_MK)
+    path = pkg.PATH_GEMV if M <= 8 else pkg.PATH_GEMM
+    Y = pkg.mul_mat_q8_1(Wd, ws, K, N, M, LAYOUT_MK, path)
+    # the ggml mmq hook (patch:299-306) on the same activations, ggml layout
+    Yg = torch.full((M, N), float("nan"), device=dev)
+    pkg.lib().check("custom_gemm_iq4xs_dispatch", Wd.data_ptr(), Xd.data_ptr(), Yg.data_ptr(), K, N, M, stream())
     torch.cuda.synchronize()
-    check_classes(orc.gemm_semantics(W, AQ, K, N, M).T, Y.cpu().numpy().reshape(M, N), f"Inf d_x, M={M}")
+    check_classes(y_ref, Y.cpu().numpy().reshape(M, N), f"Inf d_x, M={M}")
+    check_classes(y_ref, Yg.cpu().numpy(), f"Inf d_x through the mmq hook, M={M}")
+    # the rows of the token with the infinite scale are all non-finite, the other tokens' finite
+    # where the weights are
+    bad = M // 2
+    assert not np.isfinite(y_ref[bad]).any()

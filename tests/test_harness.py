@@ -68,7 +68,8 @@ def test_statistics_are_bench_h():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("op,want", [("gemv_dp4a", "gemv_iq4xs_dp4a_coop"), ("gemm_wmma", "gemm_iq4xs_wmma_stream")])
+@pytest.mark.parametrize("op,want", [("gemv", "gemv_iq4xs"), ("gemv_dp4a", "gemv_iq4xs_dp4a_coop"),
+                                     ("gemm_wmma", "gemm_iq4xs_wmma_stream")])
 def test_harness_runs_on_gpu(op, want):
     print(f"[harness] --op {op}", flush=True)
     r = subprocess.run([harness(), "--op", op, "--runs", "1"], capture_output=True, text=True, timeout=300)
