@@ -312,8 +312,8 @@ int iq4xs_q8_1_to_blocks(const void* ws, void* blocks, int64_t K, int64_t M, voi
 int iq4xs_subblock_sums(const void* W, const void* ws, int32_t* S, float* Y, int64_t K, int64_t N, int64_t M,
                         int path, void* stream);
 
-/* One v_mfma_i32_32x32x32_i8 through the GEMM's operand layouts:
- * C[i*32 + j] = sum_k A[i*32 + k] * B[j*32 + k]. */
+/* One v_mfma_i32_32x32x32_i8 through the operand and result layouts that the
+ * small-batch matrix-core GEMV relies on: C[i*32 + j] = sum_k A[i*32 + k] * B[j*32 + k]. */
 int iq4xs_probe_mfma_i8(const int8_t* A, const int8_t* B, int32_t* C, void* stream);
 
 /* ============================ synthetic inputs ============================ */
