@@ -98,7 +98,8 @@ hipError_t launch_gemm_group(int count, const uint8_t* const* W, float* const* Y
                              hipStream_t stream);
 
 // One v_mfma_i32_32x32x32_i8 on A[32][32], B[32][32] (k-contiguous rows) ->
-// C[32][32] = A B^T, through the operand layouts the GEMM uses.
+// C[32][32] = A B^T, through the operand layouts the small-batch matrix-core
+// GEMV uses.
 hipError_t launch_probe_mfma(const int8_t* A, const int8_t* B, int32_t* C, hipStream_t stream);
 
 // n_blocks super-blocks -> fp32 weights (256 per block, in block order).
