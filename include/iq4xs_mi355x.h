@@ -178,7 +178,8 @@ int custom_gemm_iq4xs_dispatch(const void* W, const float* X, float* Y, int64_t 
  * a 256-byte aligned offset: 3 * K * M + K * M / 8 bytes and padding.  Every
  * call that writes a workspace fills all three parts. */
 
-/* Bytes of workspace for M activation columns of length K. */
+/* Bytes of workspace for M activation columns of length K; 0 for shapes the
+ * entry points refuse (K not a positive multiple of 32, M < 1, K or M >= 2^31). */
 size_t iq4xs_workspace_bytes(int64_t K, int64_t M);
 
 /* X (layout IQ4XS_LAYOUT_KM or _MK) -> planar Q8_1 in ws. */

@@ -298,7 +298,7 @@ int custom_gemm_iq4xs_dispatch(const void* W, const float* X, float* Y, int64_t 
 }
 
 size_t iq4xs_workspace_bytes(int64_t K, int64_t M) {
-    if (K <= 0 || K % QK8_1 != 0 || M <= 0) return 0;
+    if (K <= 0 || K % QK8_1 != 0 || M <= 0 || K >= MAX_DIM || M >= MAX_DIM) return 0;
     return planar_bytes(K, M);
 }
 

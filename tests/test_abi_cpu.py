@@ -76,6 +76,9 @@ def test_workspace_bytes(L):
     assert L.iq4xs_workspace_bytes(K, M) == hq_off + 2 * K * M
     assert L.iq4xs_workspace_bytes(256, 1) == 256 + 256 + 512
     assert L.iq4xs_workspace_bytes(0, 1) == 0 and L.iq4xs_workspace_bytes(100, 1) == 0
+    # past the kernels' index range, as every entry point refuses (no wrapped size)
+    assert L.iq4xs_workspace_bytes(1 << 31, 1) == 0 and L.iq4xs_workspace_bytes(256, 1 << 31) == 0
+    assert L.iq4xs_workspace_bytes((1 << 31) - 32, 1) > 0
 
 
 FAKE = ctypes.c_void_p(0x100000)  # never dereferenced: every call below fails validation
